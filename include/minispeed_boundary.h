@@ -1,0 +1,207 @@
+/*
+ * minispeed_boundary.h — C ABI of the MI355X (gfx950) gradient-accumulation
+ * boundary step: the flatten / inf-nan / unscale / global-norm / clip /
+ * AdamW / master->model cast sequence that minispeed runs in
+ * DeepSpeedEngine._take_optimizer_step (minispeed/engine.py:268-322).
+ *
+ * Conventions
+ *   - Every pointer argument is caller-owned memory. Device pointers are
+ *     marked [dev]; everything else is host memory read during the call.
+ *   - Every entry point is asynchronous on the `stream` argument (a
+ *     hipStream_t passed as void*; NULL is the legacy default stream) and
+ *     allocates nothing.
+ *   - Return value: 0 on success, a negative MS_E* code for an argument
+ *     error detected on the host (nothing was launched), or a positive
+ *     hipError_t from the launch.  ms_error_string() names both kinds.
+ *   - Flat indices are "group coordinates": element k of a parameter that
+ *     starts at flat offset o has index o + k (minispeed/flat.py:81-86).
+ *     Arrays passed as `float* x` together with a range [begin, end) hold
+ *     index i at x[i - begin].
+ *   - Thread-compatible, not thread-safe: concurrent calls on different
+ *     streams must use different output buffers.
+ */
+#ifndef MINISPEED_BOUNDARY_H
+#define MINISPEED_BOUNDARY_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MS_ABI_VERSION 1
+
+/* element types of ragged gradient / model storage */
+enum {
+  MS_DTYPE_F32 = 0,
+  MS_DTYPE_F16 = 1,
+  MS_DTYPE_BF16 = 2
+};
+
+/* host-side argument errors (nothing launched) */
+enum {
+  MS_OK = 0,
+  MS_EINVAL = -1,   /* bad size, range, dtype or NULL where required */
+  MS_ETABLE = -2,   /* segment count out of range */
+  MS_EBLOCKS = -3   /* partial-sum workspace smaller than ms_stats_blocks() */
+};
+
+/*
+ * One contiguous piece of a flat group: flat indices [begin, begin+numel).
+ * `grad`  : storage of those elements' gradients in the group's grad dtype
+ *           (param.grad viewed flat, advanced to `begin`), or NULL when the
+ *           parameter has no gradient (it contributes zeros, flat.py:209-211)
+ *           or for the padding tail.
+ * `model` : storage of the model-dtype parameter elements to overwrite with
+ *           the cast of the updated fp32 master (flat.py:148-154), or NULL
+ *           when nothing is written (padding; ZeRO-3 while not gathered).
+ * A table passed to a kernel lives in device memory, is sorted by `begin`,
+ * and tiles the kernel's range exactly (no gaps, no overlap).
+ * Replaces the per-parameter (offset, numel, param) list walked by
+ * FlatParamGroup.flatten_grads / copy_flat_to_model (flat.py:78-86, 196-213,
+ * 133-154).
+ */
+typedef struct ms_segment {
+  int64_t begin;
+  int64_t numel;
+  const void* grad;
+  void* model;
+} ms_segment_t;
+
+/*
+ * Result of the boundary reduction (K2), written to device memory and read
+ * back by the host with one copy per boundary.
+ */
+typedef struct ms_step_scalars {
+  uint32_t overflow;      /* any inf/nan in the scanned grads, pre-unscale
+                             (precision.py:79-87, engine.py:275)            */
+  uint32_t clip_applied;  /* norm > max_norm and coef != 1
+                             (stage_1_and_2.py:123-126, flat.py:252-253)     */
+  float sumsq;            /* fp32 sum over groups of per-group sum of
+                             squares of the unscaled owned grads
+                             (stage_1_and_2.py:114-116)                     */
+  float norm;             /* sqrtf(sumsq) (stage_1_and_2.py:121)            */
+  float coef;             /* fp32(max_norm / (norm + 1e-6)) if clip_applied,
+                             else 1 (stage_1_and_2.py:124)                  */
+  uint32_t reserved;
+  double coef64;          /* the same coefficient before fp32 rounding      */
+  double next_scale;      /* loss scale after DynamicLossScaler.update
+                             (precision.py:50-62)                           */
+  int64_t next_good_steps;
+  int64_t next_skipped_steps;
+} ms_step_scalars_t;
+
+/*
+ * AdamW hyper-parameters for one group and one step, already rounded the
+ * way minispeed's torch op sequence rounds them (optim/adam.py:80-91):
+ * every scalar is the fp32 rounding of the double the reference computes.
+ */
+typedef struct ms_adamw_params {
+  float neg_lr;          /* fp32(-lr)                  addcdiv value      */
+  float decay_alpha;     /* fp32(-lr * weight_decay)   add_ alpha         */
+  float beta1;           /* fp32(beta1)                mul_               */
+  float one_minus_beta1; /* fp32(1 - beta1)            add_ alpha         */
+  float beta2;           /* fp32(beta2)                mul_               */
+  float one_minus_beta2; /* fp32(1 - beta2)            addcmul value      */
+  float bias_c1;         /* fp32(1 - beta1**step)      m / bias_c1        */
+  float bias_c2;         /* fp32(1 - beta2**step)      v / bias_c2        */
+  float eps;             /* fp32(eps)                  add_               */
+  float grad_scale;      /* loss scale to divide ragged grads by          */
+  int32_t decay;         /* weight_decay != 0 (adam.py:81)                */
+  int32_t unscale;       /* divide ragged grads by grad_scale (flat.py:247)*/
+} ms_adamw_params_t;
+
+/* MS_ABI_VERSION of the loaded library. */
+int ms_abi_version(void);
+
+/* Static text for a return code of this library. */
+const char* ms_error_string(int code);
+
+/* Fixed number of per-group partial slots K1 writes; a constant, so the
+ * two-level norm reduction is run-to-run deterministic. */
+int ms_stats_blocks(void);
+
+/*
+ * K1 — ragged gradient scan.  Replaces FlatParamGroup.flatten_grads
+ * (flat.py:196-213), has_overflow on the flat grad (precision.py:79-87),
+ * unscale_grads (flat.py:243-247) and local_grad_sumsq (flat.py:232-234).
+ *
+ * Scans flat indices [begin, end) through `segs` [dev] (`nseg` entries,
+ * grad dtype `grad_dtype`):
+ *   - overflow: block_flag[b] != 0 iff some grad element handled by block b
+ *     is inf/nan, tested on the raw stored value (before unscale);
+ *   - g = fp32(grad) / grad_scale when `unscale` (IEEE division), else the
+ *     exact widening fp32(grad);
+ *   - flat_grad [dev, optional]: flat_grad[i - begin] = g for every i;
+ *   - block_sumsq [dev, optional]: per-block fp64 sum of g*g over the owned
+ *     range [own_begin, own_end); with block_flag [dev] it must hold
+ *     nblk >= ms_stats_blocks() slots, and every slot is written.
+ * With block_sumsq == NULL and block_flag == NULL the call is a pure ragged
+ * flatten (FlatParamGroup.copy_model_to_flat, flat.py:115-131).
+ */
+int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
+                  int64_t begin, int64_t end, int64_t own_begin,
+                  int64_t own_end, int32_t unscale, float grad_scale,
+                  float* flat_grad, double* block_sumsq,
+                  uint32_t* block_flag, int32_t nblk, void* stream);
+
+/*
+ * K2 — global norm, clip coefficient, skip and loss-scale decision.
+ * Replaces global_overflow (precision.py:90-92), ZeROOptimizer.clip_gradients
+ * (stage_1_and_2.py:105-128) and DynamicLossScaler.update
+ * (precision.py:50-62).  One block; fixed reduction order.
+ *
+ * block_sumsq / block_flag [dev]: ngroups x nblk partials from K1 (group g
+ * at offset g*nblk).  Per group the fp64 partials are summed and rounded to
+ * fp32; the group sums are added in group order in fp32.  Clipping applies
+ * when has_clip and norm > max_norm (double compare), with
+ * coef64 = max_norm / (norm + 1e-6) and clip_applied = (coef64 != 1).
+ * The scaler fields are the state before this boundary.
+ * out [dev] receives an ms_step_scalars_t.
+ */
+int ms_norm_clip(const double* block_sumsq, const uint32_t* block_flag,
+                 int32_t nblk, int32_t ngroups, int32_t has_clip,
+                 double max_norm, int32_t scaler_enabled, double scale,
+                 int64_t good_steps, int64_t skipped_steps, int64_t window,
+                 double min_scale, double max_scale, ms_step_scalars_t* out,
+                 void* stream);
+
+/*
+ * K3 — fused AdamW over the owned range [begin, end) plus the cast of the
+ * updated masters into the model parameters.  Replaces FlatAdam.step
+ * (optim/adam.py:59-93), the clip multiply (flat.py:249-257) and
+ * copy_flat_to_model (flat.py:133-154; the ZeRO-3 placeholder refresh of
+ * stage_3.py:88-110).
+ *
+ * master, exp_avg, exp_avg_sq [dev]: fp32, index i at [i - begin].
+ * flat_grad [dev, optional]: unscaled fp32 grads at [i - begin]; when NULL
+ *   the grads are read from segs[].grad (grad_dtype) and divided by
+ *   hp->grad_scale when hp->unscale.
+ * segs [dev]: tiles [begin, end); segs[].model (model_dtype) receives the
+ *   cast of the updated master (round to nearest even).
+ * scalars [dev]: K2's output.  When scalars->overflow is set the kernel
+ *   returns without touching memory (the skipped step, engine.py:278-293);
+ *   when scalars->clip_applied the grads are multiplied by scalars->coef.
+ * hp [host]: this step's rounded hyper-parameters.
+ */
+int ms_fused_adamw(float* master, float* exp_avg, float* exp_avg_sq,
+                   const float* flat_grad, const ms_segment_t* segs,
+                   int32_t nseg, int32_t grad_dtype, int32_t model_dtype,
+                   int64_t begin, int64_t end, const ms_adamw_params_t* hp,
+                   const ms_step_scalars_t* scalars, void* stream);
+
+/*
+ * K4 — cast fp32 masters into model-dtype storage: flat [dev] holds index i
+ * at flat[i - begin]; every segment with a non-NULL `model` inside
+ * [begin, end) is written.  Replaces copy_flat_to_model (flat.py:133-154)
+ * for the ZeRO-3 gather/free casts (stage_3.py:67-110) and the skip path.
+ */
+int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
+                     const ms_segment_t* segs, int32_t nseg,
+                     int32_t model_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINISPEED_BOUNDARY_H */

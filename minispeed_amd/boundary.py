@@ -1,0 +1,221 @@
+"""The fused boundary step: K1 -> K2 -> K3 on the current HIP stream with one
+device->host read-back.
+
+Replaces the unfused sequence of minispeed's
+``DeepSpeedEngine._take_optimizer_step`` (engine.py:268-322):
+
+    flatten_grads            flat.py:196-213       \\
+    has_overflow             precision.py:79-87     > K1 per group
+    unscale_grads            flat.py:243-247       /   (+ per-block sumsq)
+    reduce_gradients         stage_1_and_2.py:86-102   identity at world 1
+    clip_gradients           stage_1_and_2.py:105-128  K2 (norm, coef, skip)
+    FlatAdam.step            optim/adam.py:59-93   \\
+    sync_parameters          stage_1_and_2.py:79-83 > K3 per group
+    (stage 3) free_parameters  stage_3.py:88-110   /
+    DynamicLossScaler.update precision.py:50-62        K2 (checked on host)
+
+K3 is gated on the device overflow flag, so the launch sequence does not
+wait for the host: the only synchronisation is the final copy of the
+``ms_step_scalars_t`` K2 wrote.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native
+from .flat import FlatParamGroup, check_table
+
+
+def _f32(x: float) -> float:
+    return float(np.float32(x))
+
+
+def adamw_params(
+    lr: float, betas: Sequence[float], eps: float, weight_decay: float, step: int,
+    grad_scale: float = 1.0, unscale: bool = False,
+) -> _native.AdamWParams:
+    """Round this step's AdamW scalars the way the torch op sequence of
+    optim/adam.py:72-91 does: every Python double becomes fp32 at the op that
+    consumes it."""
+    lr = float(lr)
+    beta1, beta2 = (float(b) for b in betas)
+    wd = float(weight_decay)
+    hp = _native.AdamWParams()
+    hp.neg_lr = _f32(-lr)
+    hp.decay_alpha = _f32(-lr * wd)
+    hp.beta1 = _f32(beta1)
+    hp.one_minus_beta1 = _f32(1.0 - beta1)
+    hp.beta2 = _f32(beta2)
+    hp.one_minus_beta2 = _f32(1.0 - beta2)
+    hp.bias_c1 = _f32(1.0 - beta1 ** step)
+    hp.bias_c2 = _f32(1.0 - beta2 ** step)
+    hp.eps = _f32(float(eps))
+    hp.grad_scale = _f32(grad_scale)
+    hp.decay = 1 if wd != 0.0 else 0
+    hp.unscale = 1 if unscale else 0
+    return hp
+
+
+class Workspace:
+    """Device scratch of the boundary step (no allocation per step)."""
+
+    def __init__(self, device: torch.device, ngroups: int):
+        self.device = device
+        self.nblk = _native.stats_blocks()
+        self.ngroups = ngroups
+        n = max(1, ngroups) * self.nblk
+        self.partials = torch.empty(n, dtype=torch.float64, device=device)
+        self.flags = torch.empty(n, dtype=torch.int32, device=device)
+        self.scalars = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=device)
+        self.host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
+
+    def partial_ptrs(self, g: int):
+        off = g * self.nblk
+        return (
+            self.partials.data_ptr() + off * 8,
+            self.flags.data_ptr() + off * 4,
+        )
+
+    def read_scalars(self) -> _native.StepScalars:
+        """Copy K2's result to pinned memory and wait for the stream."""
+        self.host.copy_(self.scalars, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
+
+
+@dataclass
+class GroupLaunch:
+    """What K1/K3 need for one group at one boundary."""
+
+    group: FlatParamGroup
+    lr: float
+    betas: Sequence[float]
+    eps: float
+    weight_decay: float
+    step: int                     # Adam step number this update would use
+    exp_avg: torch.Tensor         # owned-range moments (optim/adam.py:58-65)
+    exp_avg_sq: torch.Tensor
+    grads: List[Optional[tuple]]            # ragged grad storages (FlatParamGroup.grad_storages)
+    model: Optional[List[Optional[tuple]]]  # model storages, None: no write
+
+
+def _launch_k1(lib, ws: Workspace, gi: int, g: FlatParamGroup, grad_stores, dtype: int,
+               unscale: bool, scale: float, flat_out: Optional[torch.Tensor], stream: int) -> None:
+    n = g.numel_padded
+    table = g.layout.segments(0, n, grad_stores, [None] * len(grad_stores))
+    check_table(table, 0, n)
+    ptr, nseg = g.table("k1").upload(table)
+    psum, pflag = ws.partial_ptrs(gi)
+    lo, hi = g.own_range
+    rc = lib.ms_grad_stats(
+        ptr, nseg, dtype, 0, n, lo, hi, 1 if unscale else 0, _f32(scale),
+        flat_out.data_ptr() if flat_out is not None else None,
+        psum, pflag, ws.nblk, stream,
+    )
+    _native.check(rc, "ms_grad_stats")
+
+
+def _launch_k3(lib, ws: Workspace, gl: GroupLaunch, grad_stores, gdtype: int, mdtype: int,
+               unscale: bool, scale: float, flat_grad: Optional[torch.Tensor], stream: int) -> None:
+    g = gl.group
+    lo, hi = g.own_range
+    if hi <= lo:
+        return
+    models = gl.model if gl.model is not None else [None] * len(g.params)
+    grads = grad_stores if flat_grad is None else [None] * len(g.params)
+    table = g.layout.segments(lo, hi, grads, models)
+    check_table(table, lo, hi)
+    ptr, nseg = g.table("k3").upload(table)
+    hp = adamw_params(gl.lr, gl.betas, gl.eps, gl.weight_decay, gl.step,
+                      grad_scale=scale, unscale=unscale and flat_grad is None)
+    master = g.shard
+    if master.numel() != hi - lo or gl.exp_avg.numel() != hi - lo or gl.exp_avg_sq.numel() != hi - lo:
+        raise RuntimeError(
+            f"grad/shard shape mismatch: owned range {hi - lo} vs master {master.numel()}, "
+            f"moments {gl.exp_avg.numel()}/{gl.exp_avg_sq.numel()}"
+        )
+    fg_ptr = None
+    if flat_grad is not None:
+        fg_ptr = flat_grad.data_ptr() + lo * 4
+    rc = lib.ms_fused_adamw(
+        master.data_ptr(), gl.exp_avg.data_ptr(), gl.exp_avg_sq.data_ptr(), fg_ptr,
+        ptr, nseg, gdtype, mdtype, lo, hi, ctypes.byref(hp), ws.scalars.data_ptr(), stream,
+    )
+    _native.check(rc, "ms_fused_adamw")
+
+
+def run_boundary(
+    launches: List[GroupLaunch],
+    ws: Workspace,
+    *,
+    scaler,
+    max_norm: Optional[float],
+    materialize_flat_grad: bool,
+) -> _native.StepScalars:
+    """Launch the whole boundary and return K2's scalars (one host sync).
+
+    The caller keeps the gradient tensors behind ``GroupLaunch.grads``
+    referenced until this returns.
+    """
+    lib = _native.load()
+    device = ws.device
+    stream = _native.stream_handle(device)
+    scale = float(scaler.loss_scale_factor)
+    unscale = scale != 1.0
+
+    per_group = []
+    for gi, gl in enumerate(launches):
+        g = gl.group
+        dtype = _native.ms_dtype(g.model_dtype())
+        flat_out = None
+        if materialize_flat_grad:
+            if g.grad is None:
+                g.grad = torch.empty(g.numel_padded, dtype=torch.float32, device=device)
+            flat_out = g.grad
+            g._grad_dirty = True
+        _launch_k1(lib, ws, gi, g, gl.grads, dtype, unscale, scale, flat_out, stream)
+        per_group.append((dtype, flat_out))
+
+    rc = lib.ms_norm_clip(
+        ws.partials.data_ptr(), ws.flags.data_ptr(), ws.nblk, len(launches),
+        1 if max_norm is not None else 0, float(max_norm or 0.0),
+        1 if scaler.enabled else 0, float(scaler.scale), int(scaler.good_steps),
+        int(scaler.skipped_steps), int(scaler.scale_window),
+        float(scaler.min_scale), float(scaler.max_scale),
+        ws.scalars.data_ptr(), stream,
+    )
+    _native.check(rc, "ms_norm_clip")
+
+    for gl, (dtype, flat_out) in zip(launches, per_group):
+        _launch_k3(lib, ws, gl, gl.grads, dtype, dtype, unscale, scale, flat_out, stream)
+
+    return ws.read_scalars()
+
+
+# ------------------------------------------------------------------ utility
+def scan_nonfinite(buf: torch.Tensor) -> bool:
+    """inf/nan test of one device buffer with K1 + K2 (used by
+    precision.has_overflow)."""
+    _native.require_hip_tensor(buf, "has_overflow buffer")
+    flat = buf.detach().reshape(-1)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    n = flat.numel()
+    dtype = _native.ms_dtype(flat.dtype)
+    lib = _native.load()
+    ws = Workspace(flat.device, 1)
+    table = np.array([[0, n, flat.data_ptr(), 0]], dtype=np.int64)
+    dev_table = torch.from_numpy(table).to(flat.device)
+    stream = _native.stream_handle(flat.device)
+    psum, pflag = ws.partial_ptrs(0)
+    _native.check(lib.ms_grad_stats(dev_table.data_ptr(), 1, dtype, 0, n, 0, 0, 0, 1.0,
+                                    None, psum, pflag, ws.nblk, stream), "ms_grad_stats")
+    _native.check(lib.ms_norm_clip(psum, pflag, ws.nblk, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0,
+                                   ws.scalars.data_ptr(), stream), "ms_norm_clip")
+    return bool(ws.read_scalars().overflow)

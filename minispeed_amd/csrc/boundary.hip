@@ -1,0 +1,771 @@
+// boundary.hip — gfx950 kernels of minispeed's gradient-accumulation
+// boundary step and the C ABI declared in include/minispeed_boundary.h.
+//
+//   K1 k_grad_stats   ragged grad scan: inf/nan flag on the raw values,
+//                     unscale, optional fp32 flat write, per-block fp64
+//                     sum of squares            (flat.py:196-247)
+//   K2 k_norm_clip    deterministic second-level reduction, clip
+//                     coefficient, skip flag, loss-scale update
+//                                               (stage_1_and_2.py:105-128,
+//                                                precision.py:50-92)
+//   K3 k_adamw        fused clip + AdamW + master->model cast over the
+//                     owned range              (optim/adam.py:59-93,
+//                                                flat.py:133-154)
+//   K4 k_cast         fp32 master -> model dtype (ZeRO-3 gather/free)
+//
+// Everything here is HBM-bound streaming; no MFMA.  Work is cut into tiles
+// of kTile consecutive flat indices; a lane owns kVec consecutive elements
+// of a tile.  A tile that lies inside one segment with 16-byte aligned
+// storage takes the vector path (dwordx4 loads/stores on every stream);
+// tiles that straddle segment edges, partial tail tiles and misaligned
+// segments take the per-element path.
+//
+// Arithmetic is written so that each rounding point of minispeed's torch op
+// sequence is one IEEE fp32 operation here: the file is compiled with
+// -ffp-contract=off, products/sums that torch fuses are explicit fmaf, and
+// division and sqrt are the correctly rounded IEEE operations (HIP's
+// default `/` and sqrtf lowering, not the native approximations).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "minispeed_boundary.h"
+
+namespace {
+
+constexpr int kThreads = 256;             // 4 wave64 per block
+constexpr int kWaves = kThreads / 64;
+constexpr int kVec = 8;                   // elements per lane per tile
+constexpr int kTile = kThreads * kVec;    // 2048 flat elements
+constexpr int kStatsBlocks = 2048;        // fixed K1 grid (determinism)
+constexpr int kMaxSegs = 1 << 26;
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- dtypes
+// Raw storage <-> fp32.  Widening is exact; narrowing rounds to nearest
+// even (torch's fp32 -> fp16/bf16 copy_).  The inf/nan test looks at the
+// exponent field of the stored value, so every NaN payload and both
+// infinities count, exactly like torch.isfinite on the widened value.
+struct DF32 {
+  using raw = uint32_t;
+  static constexpr int kBytes = 4;
+  __device__ static float widen(raw r) { return __uint_as_float(r); }
+  __device__ static bool nonfinite(raw r) {
+    return (r & 0x7f800000u) == 0x7f800000u;
+  }
+  __device__ static raw narrow(float f) { return __float_as_uint(f); }
+};
+
+struct DF16 {
+  using raw = uint16_t;
+  static constexpr int kBytes = 2;
+  __device__ static float widen(raw r) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, r));
+  }
+  __device__ static bool nonfinite(raw r) { return (r & 0x7c00u) == 0x7c00u; }
+  __device__ static raw narrow(float f) {
+    return __builtin_bit_cast(raw, static_cast<_Float16>(f));
+  }
+};
+
+struct DBF16 {
+  using raw = uint16_t;
+  static constexpr int kBytes = 2;
+  __device__ static float widen(raw r) {
+    return __uint_as_float(static_cast<uint32_t>(r) << 16);
+  }
+  __device__ static bool nonfinite(raw r) { return (r & 0x7f80u) == 0x7f80u; }
+  __device__ static raw narrow(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<raw>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<raw>(u >> 16);
+  }
+};
+
+// Load / store kVec consecutive raw elements at a 16-byte aligned address.
+template <class D>
+__device__ inline void load_raw8(const void* p, typename D::raw (&r)[kVec]) {
+  if constexpr (D::kBytes == 2) {
+    u4 w = *reinterpret_cast<const u4*>(p);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r[2 * k] = static_cast<uint16_t>(w[k] & 0xffffu);
+      r[2 * k + 1] = static_cast<uint16_t>(w[k] >> 16);
+    }
+  } else {
+    const u4* q = reinterpret_cast<const u4*>(p);
+    u4 a = q[0], b = q[1];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r[k] = a[k];
+      r[4 + k] = b[k];
+    }
+  }
+}
+
+template <class D>
+__device__ inline void store_raw8(void* p, const typename D::raw (&r)[kVec]) {
+  if constexpr (D::kBytes == 2) {
+    u4 w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = static_cast<uint32_t>(r[2 * k]) |
+             (static_cast<uint32_t>(r[2 * k + 1]) << 16);
+    *reinterpret_cast<u4*>(p) = w;
+  } else {
+    u4* q = reinterpret_cast<u4*>(p);
+    u4 a, b;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a[k] = r[k];
+      b[k] = r[4 + k];
+    }
+    q[0] = a;
+    q[1] = b;
+  }
+}
+
+__device__ inline void load_f8(const float* p, float (&x)[kVec]) {
+  const f4* q = reinterpret_cast<const f4*>(p);
+  f4 a = q[0], b = q[1];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    x[k] = a[k];
+    x[4 + k] = b[k];
+  }
+}
+
+__device__ inline void store_f8(float* p, const float (&x)[kVec]) {
+  f4* q = reinterpret_cast<f4*>(p);
+  f4 a, b;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    a[k] = x[k];
+    b[k] = x[4 + k];
+  }
+  q[0] = a;
+  q[1] = b;
+}
+
+template <class D>
+__device__ inline typename D::raw load_raw1(const void* base, int64_t k) {
+  return reinterpret_cast<const typename D::raw*>(base)[k];
+}
+
+template <class D>
+__device__ inline void store_raw1(void* base, int64_t k, typename D::raw v) {
+  reinterpret_cast<typename D::raw*>(base)[k] = v;
+}
+
+__device__ inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Largest s with segs[s].begin <= i (segs sorted, segs[0].begin <= i).
+__device__ inline int find_seg(const ms_segment_t* segs, int nseg, int64_t i) {
+  int lo = 0, hi = nseg - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (segs[mid].begin <= i)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+__device__ inline int64_t seg_end(const ms_segment_t& s) {
+  return s.begin + s.numel;
+}
+
+// ------------------------------------------------------- block reductions
+__device__ inline double wave_sum(double x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// ------------------------------------------------------------------ K1
+// One partial per block.  Blocks walk tiles t = blockIdx.x + k * gridDim.x
+// (gridDim.x == kStatsBlocks, a constant), lanes accumulate their own
+// elements in index order, waves reduce with a fixed xor tree and the four
+// wave sums are added in wave order: the partials, and hence the norm, are
+// bitwise reproducible.
+template <class G, bool kFlat, bool kStats>
+__global__ __launch_bounds__(kThreads) void k_grad_stats(
+    const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
+    int64_t end, int64_t own_begin, int64_t own_end, int unscale,
+    float grad_scale, float* __restrict__ flat, double* __restrict__ bsum,
+    uint32_t* __restrict__ bflag) {
+  const int lane = threadIdx.x;
+  double acc = 0.0;
+  bool bad = false;
+  const int64_t n = end - begin;
+  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const bool flat_vec = !kFlat || aligned16(flat);
+
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    const int64_t t0 = begin + t * kTile;
+    const int64_t t1 = (t0 + kTile < end) ? t0 + kTile : end;
+    int s = find_seg(segs, nseg, t0);
+    const ms_segment_t seg = segs[s];
+    const bool own_all = t0 >= own_begin && t1 <= own_end;
+    const bool fast = t1 - t0 == kTile && t0 >= seg.begin && t1 <= seg_end(seg) && flat_vec &&
+                      ((t0 - seg.begin) & (kVec - 1)) == 0 &&
+                      aligned16(seg.grad) && own_all;
+    const int64_t i0 = t0 + static_cast<int64_t>(lane) * kVec;
+    if (fast) {
+      float g[kVec];
+      if (seg.grad) {
+        typename G::raw r[kVec];
+        load_raw8<G>(static_cast<const char*>(seg.grad) +
+                         (i0 - seg.begin) * G::kBytes,
+                     r);
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) {
+          bad |= G::nonfinite(r[k]);
+          g[k] = G::widen(r[k]);
+          if (unscale) g[k] = g[k] / grad_scale;
+          if (kStats) {
+            const double d = static_cast<double>(g[k]);
+            acc = __builtin_fma(d, d, acc);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) g[k] = 0.0f;
+      }
+      if (kFlat) store_f8(flat + (i0 - begin), g);
+    } else {
+      int sl = s;
+      for (int k = 0; k < kVec; ++k) {
+        const int64_t i = i0 + k;
+        if (i >= t1) break;
+        while (sl + 1 < nseg && i >= seg_end(segs[sl])) ++sl;
+        const ms_segment_t& sg = segs[sl];
+        const bool inside = i >= sg.begin && i < seg_end(sg);
+        float g = 0.0f;
+        if (inside && sg.grad) {
+          const typename G::raw r = load_raw1<G>(sg.grad, i - sg.begin);
+          bad |= G::nonfinite(r);
+          g = G::widen(r);
+          if (unscale) g = g / grad_scale;
+        }
+        if (kStats && i >= own_begin && i < own_end) {
+          const double d = static_cast<double>(g);
+          acc = __builtin_fma(d, d, acc);
+        }
+        if (kFlat) flat[i - begin] = g;
+      }
+    }
+  }
+
+  if (kStats) {
+    __shared__ double wsum[kWaves];
+    __shared__ uint32_t wbad[kWaves];
+    const double w = wave_sum(acc);
+    const bool wb = __any(bad);
+    if ((lane & 63) == 0) {
+      wsum[lane >> 6] = w;
+      wbad[lane >> 6] = wb ? 1u : 0u;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      double total = 0.0;
+      uint32_t flag = 0;
+#pragma unroll
+      for (int k = 0; k < kWaves; ++k) {
+        total += wsum[k];
+        flag |= wbad[k];
+      }
+      bsum[blockIdx.x] = total;
+      bflag[blockIdx.x] = flag;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ K2
+__global__ __launch_bounds__(kThreads) void k_norm_clip(
+    const double* __restrict__ bsum, const uint32_t* __restrict__ bflag,
+    int nblk, int ngroups, int has_clip, double max_norm, int scaler_enabled,
+    double scale, int64_t good_steps, int64_t skipped_steps, int64_t window,
+    double min_scale, double max_scale, ms_step_scalars_t* __restrict__ out) {
+  __shared__ double wsum[kWaves];
+  __shared__ uint32_t wbad[kWaves];
+  const int tid = threadIdx.x;
+  float total = 0.0f;      // meaningful in thread 0
+  uint32_t overflow = 0;   // meaningful in thread 0
+  for (int gi = 0; gi < ngroups; ++gi) {
+    const double* ps = bsum + static_cast<int64_t>(gi) * nblk;
+    const uint32_t* pf = bflag + static_cast<int64_t>(gi) * nblk;
+    double acc = 0.0;
+    uint32_t bad = 0;
+    for (int b = tid; b < nblk; b += kThreads) {
+      acc += ps[b];
+      bad |= pf[b];
+    }
+    const double w = wave_sum(acc);
+    const bool wb = __any(bad != 0);
+    if ((tid & 63) == 0) {
+      wsum[tid >> 6] = w;
+      wbad[tid >> 6] = wb ? 1u : 0u;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      double gsum = 0.0;
+      for (int k = 0; k < kWaves; ++k) {
+        gsum += wsum[k];
+        overflow |= wbad[k];
+      }
+      // per-group fp32 sum of squares, accumulated over groups in fp32
+      total = total + static_cast<float>(gsum);
+    }
+    __syncthreads();
+  }
+  if (tid != 0) return;
+
+  ms_step_scalars_t r;
+  r.overflow = overflow ? 1u : 0u;
+  r.reserved = 0;
+  r.sumsq = total;
+  r.norm = sqrtf(total);
+  r.clip_applied = 0;
+  r.coef = 1.0f;
+  r.coef64 = 1.0;
+  double next_scale = scale;
+  int64_t good = good_steps, skipped = skipped_steps;
+  if (overflow) {
+    if (scaler_enabled) {
+      const double half = scale / 2.0;
+      next_scale = half > min_scale ? half : min_scale;
+      good = 0;
+      skipped += 1;
+    }
+  } else {
+    const double norm = static_cast<double>(r.norm);
+    if (has_clip && norm > max_norm) {
+      const double coef = max_norm / (norm + 1e-6);
+      r.coef64 = coef;
+      if (coef != 1.0) {
+        r.clip_applied = 1;
+        r.coef = static_cast<float>(coef);
+      }
+    }
+    if (scaler_enabled) {
+      good += 1;
+      if (good >= window && scale < max_scale) {
+        const double twice = scale * 2.0;
+        next_scale = twice < max_scale ? twice : max_scale;
+        good = 0;
+      }
+    }
+  }
+  r.next_scale = next_scale;
+  r.next_good_steps = good;
+  r.next_skipped_steps = skipped;
+  *out = r;
+}
+
+// ------------------------------------------------------------------ K3
+struct AdamScalars {
+  float neg_lr, decay_alpha, beta1, omb1, beta2, omb2, bc1, bc2, eps,
+      grad_scale;
+  int decay, unscale;
+};
+
+// One AdamW element, rounding exactly where minispeed's op sequence rounds
+// (optim/adam.py:82-91 on top of flat.py:247 and flat.py:255-257):
+//   g  = g / scale                      div_          (optional)
+//   g  = g * coef                       mul_          (clip, optional)
+//   p  = fma(p, -lr*wd, p)              add_(alpha)   (decay, optional)
+//   m  = fma(g, 1-b1, m*b1)             mul_, add_(alpha)
+//   v  = fma((1-b2)*g, g, v*b2)         mul_, addcmul_
+//   d  = sqrt(v / bc2) + eps            div, sqrt, add_
+//   p  = p + ((-lr) * (m / bc1)) / d    div, addcdiv_
+__device__ inline void adamw1(float g, float& p, float& m, float& v,
+                              const AdamScalars& h, bool clip, float coef) {
+  if (clip) g = g * coef;
+  if (h.decay) p = __builtin_fmaf(p, h.decay_alpha, p);
+  m = __builtin_fmaf(g, h.omb1, m * h.beta1);
+  v = __builtin_fmaf(h.omb2 * g, g, v * h.beta2);
+  const float den = sqrtf(v / h.bc2) + h.eps;
+  p = p + (h.neg_lr * (m / h.bc1)) / den;
+}
+
+template <class G, class M, bool kFlatGrad>
+__global__ __launch_bounds__(kThreads) void k_adamw(
+    float* __restrict__ master, float* __restrict__ exp_avg,
+    float* __restrict__ exp_avg_sq, const float* __restrict__ flat_grad,
+    const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
+    int64_t end, AdamScalars h, const ms_step_scalars_t* __restrict__ sc) {
+  if (sc->overflow) return;   // skipped step: nothing is touched
+  const bool clip = sc->clip_applied != 0;
+  const float coef = sc->coef;
+  const int lane = threadIdx.x;
+  const int64_t n = end - begin;
+  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const bool arrays_vec = aligned16(master) && aligned16(exp_avg) &&
+                          aligned16(exp_avg_sq) &&
+                          (!kFlatGrad || aligned16(flat_grad));
+
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    const int64_t t0 = begin + t * kTile;
+    const int64_t t1 = (t0 + kTile < end) ? t0 + kTile : end;
+    const int s = find_seg(segs, nseg, t0);
+    const ms_segment_t seg = segs[s];
+    const bool fast = t1 - t0 == kTile && t0 >= seg.begin && t1 <= seg_end(seg) && arrays_vec &&
+                      ((t0 - seg.begin) & (kVec - 1)) == 0 &&
+                      (kFlatGrad || aligned16(seg.grad)) && aligned16(seg.model);
+    const int64_t i0 = t0 + static_cast<int64_t>(lane) * kVec;
+    const int64_t li = i0 - begin;
+    if (fast) {
+      float g[kVec], p[kVec], m[kVec], v[kVec];
+      if (kFlatGrad) {
+        load_f8(flat_grad + li, g);
+      } else if (seg.grad) {
+        typename G::raw r[kVec];
+        load_raw8<G>(static_cast<const char*>(seg.grad) +
+                         (i0 - seg.begin) * G::kBytes,
+                     r);
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) {
+          g[k] = G::widen(r[k]);
+          if (h.unscale) g[k] = g[k] / h.grad_scale;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) g[k] = 0.0f;
+      }
+      load_f8(master + li, p);
+      load_f8(exp_avg + li, m);
+      load_f8(exp_avg_sq + li, v);
+#pragma unroll
+      for (int k = 0; k < kVec; ++k) adamw1(g[k], p[k], m[k], v[k], h, clip, coef);
+      store_f8(master + li, p);
+      store_f8(exp_avg + li, m);
+      store_f8(exp_avg_sq + li, v);
+      if (seg.model) {
+        typename M::raw o[kVec];
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) o[k] = M::narrow(p[k]);
+        store_raw8<M>(static_cast<char*>(seg.model) +
+                          (i0 - seg.begin) * M::kBytes,
+                      o);
+      }
+    } else {
+      int sl = s;
+      for (int k = 0; k < kVec; ++k) {
+        const int64_t i = i0 + k;
+        if (i >= t1) break;
+        while (sl + 1 < nseg && i >= seg_end(segs[sl])) ++sl;
+        const ms_segment_t& sg = segs[sl];
+        const bool inside = i >= sg.begin && i < seg_end(sg);
+        const int64_t l = i - begin;
+        float g = 0.0f;
+        if (kFlatGrad) {
+          g = flat_grad[l];
+        } else if (inside && sg.grad) {
+          g = G::widen(load_raw1<G>(sg.grad, i - sg.begin));
+          if (h.unscale) g = g / h.grad_scale;
+        }
+        float p = master[l], m = exp_avg[l], v = exp_avg_sq[l];
+        adamw1(g, p, m, v, h, clip, coef);
+        master[l] = p;
+        exp_avg[l] = m;
+        exp_avg_sq[l] = v;
+        if (inside && sg.model) store_raw1<M>(sg.model, i - sg.begin, M::narrow(p));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ K4
+template <class M>
+__global__ __launch_bounds__(kThreads) void k_cast(
+    const float* __restrict__ flat, const ms_segment_t* __restrict__ segs,
+    int nseg, int64_t begin, int64_t end) {
+  const int lane = threadIdx.x;
+  const int64_t n = end - begin;
+  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const bool flat_vec = aligned16(flat);
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    const int64_t t0 = begin + t * kTile;
+    const int64_t t1 = (t0 + kTile < end) ? t0 + kTile : end;
+    const int s = find_seg(segs, nseg, t0);
+    const ms_segment_t seg = segs[s];
+    const bool fast = t1 - t0 == kTile && t0 >= seg.begin && t1 <= seg_end(seg) && flat_vec &&
+                      ((t0 - seg.begin) & (kVec - 1)) == 0 &&
+                      aligned16(seg.model);
+    const int64_t i0 = t0 + static_cast<int64_t>(lane) * kVec;
+    if (fast) {
+      if (!seg.model) continue;
+      float x[kVec];
+      load_f8(flat + (i0 - begin), x);
+      typename M::raw o[kVec];
+#pragma unroll
+      for (int k = 0; k < kVec; ++k) o[k] = M::narrow(x[k]);
+      store_raw8<M>(static_cast<char*>(seg.model) + (i0 - seg.begin) * M::kBytes,
+                    o);
+    } else {
+      int sl = s;
+      for (int k = 0; k < kVec; ++k) {
+        const int64_t i = i0 + k;
+        if (i >= t1) break;
+        while (sl + 1 < nseg && i >= seg_end(segs[sl])) ++sl;
+        const ms_segment_t& sg = segs[sl];
+        if (i >= sg.begin && i < seg_end(sg) && sg.model)
+          store_raw1<M>(sg.model, i - sg.begin, M::narrow(flat[i - begin]));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- launching
+int cu_count() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+            hipSuccess &&
+        n > 0)
+      cached = n;
+    else
+      cached = 256;
+  }
+  return cached;
+}
+
+// Grid of a streaming kernel: enough resident blocks to keep every CU's
+// memory pipeline full, never more blocks than tiles.
+int stream_grid(int64_t ntiles, int blocks_per_cu) {
+  int64_t g = static_cast<int64_t>(cu_count()) * blocks_per_cu;
+  if (g > ntiles) g = ntiles;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
+int env_int(const char* name, int fallback) {
+  const char* s = getenv(name);
+  if (!s || !*s) return fallback;
+  const int v = atoi(s);
+  return v > 0 ? v : fallback;
+}
+
+int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MS_OK : static_cast<int>(e);
+}
+
+bool valid_dtype(int32_t d) {
+  return d == MS_DTYPE_F32 || d == MS_DTYPE_F16 || d == MS_DTYPE_BF16;
+}
+
+template <class G>
+void launch_stats(const ms_segment_t* segs, int nseg, int64_t begin,
+                  int64_t end, int64_t ob, int64_t oe, int unscale, float scale,
+                  float* flat, double* bsum, uint32_t* bflag, hipStream_t st) {
+  const bool stats = bsum != nullptr;
+  const int64_t ntiles = (end - begin + kTile - 1) / kTile;
+  const dim3 block(kThreads);
+  if (stats) {
+    const dim3 grid(kStatsBlocks);
+    if (flat)
+      hipLaunchKernelGGL((k_grad_stats<G, true, true>), grid, block, 0, st, segs,
+                         nseg, begin, end, ob, oe, unscale, scale, flat, bsum,
+                         bflag);
+    else
+      hipLaunchKernelGGL((k_grad_stats<G, false, true>), grid, block, 0, st,
+                         segs, nseg, begin, end, ob, oe, unscale, scale, flat,
+                         bsum, bflag);
+  } else {
+    const dim3 grid(stream_grid(ntiles, env_int("MS_FLATTEN_BLOCKS_PER_CU", 8)));
+    hipLaunchKernelGGL((k_grad_stats<G, true, false>), grid, block, 0, st, segs,
+                       nseg, begin, end, ob, oe, unscale, scale, flat, bsum,
+                       bflag);
+  }
+}
+
+template <class G, class M>
+void launch_adamw(float* p, float* m, float* v, const float* fg,
+                  const ms_segment_t* segs, int nseg, int64_t begin, int64_t end,
+                  const AdamScalars& h, const ms_step_scalars_t* sc,
+                  hipStream_t st) {
+  const int64_t ntiles = (end - begin + kTile - 1) / kTile;
+  const dim3 grid(stream_grid(ntiles, env_int("MS_ADAMW_BLOCKS_PER_CU", 8)));
+  const dim3 block(kThreads);
+  if (fg)
+    hipLaunchKernelGGL((k_adamw<G, M, true>), grid, block, 0, st, p, m, v, fg,
+                       segs, nseg, begin, end, h, sc);
+  else
+    hipLaunchKernelGGL((k_adamw<G, M, false>), grid, block, 0, st, p, m, v, fg,
+                       segs, nseg, begin, end, h, sc);
+}
+
+template <class G>
+void launch_adamw_m(int32_t model_dtype, float* p, float* m, float* v,
+                    const float* fg, const ms_segment_t* segs, int nseg,
+                    int64_t begin, int64_t end, const AdamScalars& h,
+                    const ms_step_scalars_t* sc, hipStream_t st) {
+  switch (model_dtype) {
+    case MS_DTYPE_F32:
+      launch_adamw<G, DF32>(p, m, v, fg, segs, nseg, begin, end, h, sc, st);
+      break;
+    case MS_DTYPE_F16:
+      launch_adamw<G, DF16>(p, m, v, fg, segs, nseg, begin, end, h, sc, st);
+      break;
+    default:
+      launch_adamw<G, DBF16>(p, m, v, fg, segs, nseg, begin, end, h, sc, st);
+      break;
+  }
+}
+
+}  // namespace
+
+// =================================================================== C ABI
+extern "C" {
+
+int ms_abi_version(void) { return MS_ABI_VERSION; }
+
+const char* ms_error_string(int code) {
+  switch (code) {
+    case MS_OK:
+      return "success";
+    case MS_EINVAL:
+      return "invalid argument (size, range, dtype or required pointer)";
+    case MS_ETABLE:
+      return "segment count out of range";
+    case MS_EBLOCKS:
+      return "partial-sum workspace smaller than ms_stats_blocks()";
+    default:
+      break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "unknown error";
+}
+
+int ms_stats_blocks(void) { return kStatsBlocks; }
+
+int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
+                  int64_t begin, int64_t end, int64_t own_begin,
+                  int64_t own_end, int32_t unscale, float grad_scale,
+                  float* flat_grad, double* block_sumsq,
+                  uint32_t* block_flag, int32_t nblk, void* stream) {
+  if (!valid_dtype(grad_dtype) || begin < 0 || end < begin) return MS_EINVAL;
+  if ((block_sumsq == nullptr) != (block_flag == nullptr)) return MS_EINVAL;
+  if (block_sumsq == nullptr && flat_grad == nullptr) return MS_EINVAL;
+  if (block_sumsq != nullptr && nblk < kStatsBlocks) return MS_EBLOCKS;
+  if (end > begin && (segs == nullptr || nseg <= 0)) return MS_ETABLE;
+  if (nseg < 0 || nseg > kMaxSegs) return MS_ETABLE;
+  if (unscale && !(grad_scale > 0.0f)) return MS_EINVAL;
+  if (block_sumsq == nullptr && end == begin) return MS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (grad_dtype) {
+    case MS_DTYPE_F32:
+      launch_stats<DF32>(segs, nseg, begin, end, own_begin, own_end, unscale,
+                         grad_scale, flat_grad, block_sumsq, block_flag, st);
+      break;
+    case MS_DTYPE_F16:
+      launch_stats<DF16>(segs, nseg, begin, end, own_begin, own_end, unscale,
+                         grad_scale, flat_grad, block_sumsq, block_flag, st);
+      break;
+    default:
+      launch_stats<DBF16>(segs, nseg, begin, end, own_begin, own_end, unscale,
+                          grad_scale, flat_grad, block_sumsq, block_flag, st);
+      break;
+  }
+  return launch_status();
+}
+
+int ms_norm_clip(const double* block_sumsq, const uint32_t* block_flag,
+                 int32_t nblk, int32_t ngroups, int32_t has_clip,
+                 double max_norm, int32_t scaler_enabled, double scale,
+                 int64_t good_steps, int64_t skipped_steps, int64_t window,
+                 double min_scale, double max_scale, ms_step_scalars_t* out,
+                 void* stream) {
+  if (!block_sumsq || !block_flag || !out || ngroups < 0) return MS_EINVAL;
+  if (nblk < kStatsBlocks) return MS_EBLOCKS;
+  if (window < 1) return MS_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_norm_clip, dim3(1), dim3(kThreads), 0, st, block_sumsq,
+                     block_flag, nblk, ngroups, has_clip, max_norm,
+                     scaler_enabled, scale, good_steps, skipped_steps, window,
+                     min_scale, max_scale, out);
+  return launch_status();
+}
+
+int ms_fused_adamw(float* master, float* exp_avg, float* exp_avg_sq,
+                   const float* flat_grad, const ms_segment_t* segs,
+                   int32_t nseg, int32_t grad_dtype, int32_t model_dtype,
+                   int64_t begin, int64_t end, const ms_adamw_params_t* hp,
+                   const ms_step_scalars_t* scalars, void* stream) {
+  if (!valid_dtype(grad_dtype) || !valid_dtype(model_dtype)) return MS_EINVAL;
+  if (!hp || !scalars || begin < 0 || end < begin) return MS_EINVAL;
+  if (end == begin) return MS_OK;
+  if (!master || !exp_avg || !exp_avg_sq) return MS_EINVAL;
+  if (!segs || nseg <= 0 || nseg > kMaxSegs) return MS_ETABLE;
+  if (hp->unscale && !(hp->grad_scale > 0.0f)) return MS_EINVAL;
+  AdamScalars h;
+  h.neg_lr = hp->neg_lr;
+  h.decay_alpha = hp->decay_alpha;
+  h.beta1 = hp->beta1;
+  h.omb1 = hp->one_minus_beta1;
+  h.beta2 = hp->beta2;
+  h.omb2 = hp->one_minus_beta2;
+  h.bc1 = hp->bias_c1;
+  h.bc2 = hp->bias_c2;
+  h.eps = hp->eps;
+  h.grad_scale = hp->grad_scale;
+  h.decay = hp->decay != 0;
+  h.unscale = hp->unscale != 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (grad_dtype) {
+    case MS_DTYPE_F32:
+      launch_adamw_m<DF32>(model_dtype, master, exp_avg, exp_avg_sq, flat_grad,
+                           segs, nseg, begin, end, h, scalars, st);
+      break;
+    case MS_DTYPE_F16:
+      launch_adamw_m<DF16>(model_dtype, master, exp_avg, exp_avg_sq, flat_grad,
+                           segs, nseg, begin, end, h, scalars, st);
+      break;
+    default:
+      launch_adamw_m<DBF16>(model_dtype, master, exp_avg, exp_avg_sq, flat_grad,
+                            segs, nseg, begin, end, h, scalars, st);
+      break;
+  }
+  return launch_status();
+}
+
+int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
+                     const ms_segment_t* segs, int32_t nseg,
+                     int32_t model_dtype, void* stream) {
+  if (!valid_dtype(model_dtype) || begin < 0 || end < begin) return MS_EINVAL;
+  if (end == begin) return MS_OK;
+  if (!flat) return MS_EINVAL;
+  if (!segs || nseg <= 0 || nseg > kMaxSegs) return MS_ETABLE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t ntiles = (end - begin + kTile - 1) / kTile;
+  const dim3 grid(stream_grid(ntiles, env_int("MS_CAST_BLOCKS_PER_CU", 8)));
+  const dim3 block(kThreads);
+  switch (model_dtype) {
+    case MS_DTYPE_F32:
+      hipLaunchKernelGGL(k_cast<DF32>, grid, block, 0, st, flat, segs, nseg,
+                         begin, end);
+      break;
+    case MS_DTYPE_F16:
+      hipLaunchKernelGGL(k_cast<DF16>, grid, block, 0, st, flat, segs, nseg,
+                         begin, end);
+      break;
+    default:
+      hipLaunchKernelGGL(k_cast<DBF16>, grid, block, 0, st, flat, segs, nseg,
+                         begin, end);
+      break;
+  }
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,467 @@
+"""Flat fp32 parameter groups (the layout of minispeed/flat.py).
+
+A parameter group is laid out as one flat index space: parameter ``i`` owns
+``[offset_i, offset_i + numel_i)`` with ``offset_i`` the prefix sum of the
+numels in group order, and the space is zero-padded to
+``numel_padded = round_up(numel, world_size)`` (flat.py:16-17, 50-52).  Rank
+``r`` owns ``[r*S, (r+1)*S)`` with ``S = numel_padded / world_size`` for
+ZeRO stage >= 1 and the whole space at stage 0 (flat.py:54-59).
+
+Device buffers, all fp32 and resident in HBM (flat.py:61-73):
+  ``data``        masters, ``numel_padded`` (the owned shard only after a
+                  ZeRO-3 ``partition_params``)
+  ``grad``        flat gradient, ``numel_padded`` (stage 3: ``None`` outside
+                  the boundary)
+  ``grad_shard``  owned gradient slice, stage >= 2
+
+The boundary kernels address ragged per-parameter storage (``param.grad``,
+``param.data``) through segment tables built by :class:`FlatLayout`; a table
+is a sorted list of ``(begin, numel, grad_ptr, model_ptr)`` rows that tiles a
+flat range exactly, gaps and padding being rows with NULL pointers.
+"""
+
+from __future__ import annotations
+
+from typing import Iterable, List, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+from torch import nn
+
+from . import _native
+
+Range = Tuple[int, int]
+
+
+def _round_up(x: int, multiple: int) -> int:
+    return -(-x // multiple) * multiple
+
+
+def _overlap(a: Range, b: Range) -> Range:
+    lo, hi = max(a[0], b[0]), min(a[1], b[1])
+    return (lo, hi) if lo < hi else (lo, lo)
+
+
+# --------------------------------------------------------------------------
+class FlatLayout:
+    """Index math of one flat group; no device memory, CPU-testable."""
+
+    def __init__(self, numels: Sequence[int], *, rank: int, world_size: int, zero_stage: int):
+        if len(numels) == 0:
+            raise ValueError("FlatParamGroup requires at least one parameter")
+        if world_size < 1 or not (0 <= rank < world_size):
+            raise ValueError(f"bad rank/world_size {rank}/{world_size}")
+        self.numels: List[int] = [int(n) for n in numels]
+        self.offsets: List[int] = []
+        acc = 0
+        for n in self.numels:
+            self.offsets.append(acc)
+            acc += n
+        self.numel = acc
+        self.numel_padded = _round_up(acc, world_size)
+        self.shard_size = self.numel_padded // world_size
+        if zero_stage >= 1:
+            self.shard_start = rank * self.shard_size
+            self.shard_end = self.shard_start + self.shard_size
+        else:
+            self.shard_start, self.shard_end = 0, self.numel_padded
+
+    def param_range(self, i: int) -> Range:
+        return self.offsets[i], self.offsets[i] + self.numels[i]
+
+    def segments(
+        self,
+        lo: int,
+        hi: int,
+        grads: Sequence[Optional[Tuple[int, Range, int]]],
+        models: Sequence[Optional[Tuple[int, Range, int]]],
+    ) -> np.ndarray:
+        """Segment table tiling ``[lo, hi)``.
+
+        ``grads[i]`` / ``models[i]`` describe parameter ``i``'s gradient and
+        model storage as ``(base_ptr, (flat_begin, flat_end), elem_bytes)``:
+        element ``j`` of the flat range lives at
+        ``base_ptr + (j - flat_begin) * elem_bytes``; ``None`` means no such
+        storage.  Rows are cut wherever either storage starts or ends, so
+        every row has one grad pointer and one model pointer (or NULL).
+        """
+        fast = self._segments_whole(lo, hi, grads, models)
+        if fast is not None:
+            return fast
+        rows: List[Tuple[int, int, int, int]] = []
+
+        def emit(b: int, e: int, g: int, m: int) -> None:
+            if e <= b:
+                return
+            if rows and rows[-1][0] + rows[-1][1] == b and rows[-1][2] == 0 and rows[-1][3] == 0 \
+                    and g == 0 and m == 0:
+                prev = rows[-1]
+                rows[-1] = (prev[0], prev[1] + (e - b), 0, 0)
+                return
+            rows.append((b, e - b, g, m))
+
+        cursor = lo
+        for i in range(len(self.numels)):
+            pb, pe = _overlap(self.param_range(i), (lo, hi))
+            if pb >= pe:
+                continue
+            cuts = {pb, pe}
+            for store in (grads[i], models[i]):
+                if store is not None:
+                    sb, se = _overlap(store[1], (pb, pe))
+                    if sb < se:
+                        cuts.update((sb, se))
+            pts = sorted(cuts)
+            for b, e in zip(pts[:-1], pts[1:]):
+                gp = mp = 0
+                g = grads[i]
+                if g is not None and g[1][0] <= b and e <= g[1][1]:
+                    gp = g[0] + (b - g[1][0]) * g[2]
+                m = models[i]
+                if m is not None and m[1][0] <= b and e <= m[1][1]:
+                    mp = m[0] + (b - m[1][0]) * m[2]
+                if b > cursor:
+                    emit(cursor, b, 0, 0)
+                emit(b, e, gp, mp)
+                cursor = e
+        if cursor < hi:
+            emit(cursor, hi, 0, 0)
+        table = np.zeros((len(rows), 4), dtype=np.int64)
+        if rows:
+            table[:] = np.asarray(rows, dtype=np.uint64).astype(np.int64)
+        return table
+
+    def _segments_whole(self, lo, hi, grads, models) -> Optional[np.ndarray]:
+        """Table for the common case: the range is the whole padded space and
+        every storage covers exactly its parameter (one row per non-empty
+        parameter plus one padding row).  ``None`` when that does not hold."""
+        if lo != 0 or hi != self.numel_padded:
+            return None
+        rows = []
+        for i, (off, n) in enumerate(zip(self.offsets, self.numels)):
+            g, m = grads[i], models[i]
+            if (g is not None and g[1] != (off, off + n)) or (m is not None and m[1] != (off, off + n)):
+                return None
+            if n:
+                rows.append((off, n, g[0] if g is not None else 0, m[0] if m is not None else 0))
+        if self.numel_padded > self.numel:
+            rows.append((self.numel, self.numel_padded - self.numel, 0, 0))
+        table = np.zeros((len(rows), 4), dtype=np.int64)
+        if rows:
+            table[:] = np.asarray(rows, dtype=np.uint64).astype(np.int64)
+        return table
+
+
+def check_table(table: np.ndarray, lo: int, hi: int) -> None:
+    """Assert that a segment table tiles ``[lo, hi)`` (host-side guard run
+    before every upload, so the kernels' segment walks stay in bounds)."""
+    if hi <= lo:
+        return
+    if table.shape[0] == 0:
+        raise RuntimeError("empty segment table for a non-empty range")
+    begins, numels = table[:, 0], table[:, 1]
+    if begins[0] != lo or begins[-1] + numels[-1] != hi:
+        raise RuntimeError("segment table does not cover its range")
+    if np.any(numels <= 0) or np.any(begins[1:] != begins[:-1] + numels[:-1]):
+        raise RuntimeError("segment table rows are not contiguous")
+
+
+class SegmentTable:
+    """Device copy of a segment table, re-uploaded only when it changes.
+
+    Uploads go through a fresh pinned host tensor with a non-blocking copy on
+    the current stream; torch's host allocator keeps that staging memory
+    until the copy has run, and the copy is stream-ordered before the
+    kernels that read the table.
+    """
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self._host: Optional[np.ndarray] = None
+        self._dev: Optional[torch.Tensor] = None
+
+    def upload(self, table: np.ndarray) -> Tuple[int, int]:
+        """Return (device pointer, row count)."""
+        n = int(table.shape[0])
+        if n == 0:
+            return 0, 0
+        if self._host is not None and self._host.shape == table.shape and np.array_equal(self._host, table):
+            return self._dev.data_ptr(), n
+        staging = torch.empty((n, 4), dtype=torch.int64, pin_memory=True)
+        staging.numpy()[:] = table
+        if self._dev is None or self._dev.shape[0] != n:
+            self._dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
+        self._dev.copy_(staging, non_blocking=True)
+        self._host = table.copy()
+        return self._dev.data_ptr(), n
+
+
+def _flat_view(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+# --------------------------------------------------------------------------
+class FlatParamGroup:
+    """One parameter group flattened into contiguous fp32 HBM buffers.
+
+    Attributes and methods follow minispeed/flat.py:20-260; the data
+    movement (ragged flatten, master->model casts) runs as HIP kernels of the
+    boundary library.
+    """
+
+    def __init__(
+        self,
+        params: Sequence[nn.Parameter],
+        *,
+        rank: int,
+        world_size: int,
+        zero_stage: int,
+        device: torch.device,
+    ):
+        device = torch.device(device)
+        if len(params) == 0:
+            raise ValueError("FlatParamGroup requires at least one parameter")
+        if device.type != "cuda":
+            raise RuntimeError(
+                f"FlatParamGroup on {device}: the flat buffers live in HBM and are "
+                "updated by HIP kernels; use a ROCm GPU device"
+            )
+        self.params: List[nn.Parameter] = list(params)
+        self.zero_stage = zero_stage
+        self.device = device
+        self.layout = FlatLayout(
+            [p.numel() for p in self.params], rank=rank, world_size=world_size, zero_stage=zero_stage
+        )
+        lay = self.layout
+        self.numel = lay.numel
+        self.numel_padded = lay.numel_padded
+        self.shard_size = lay.shard_size
+        self.shard_start, self.shard_end = lay.shard_start, lay.shard_end
+
+        self.data = torch.zeros(self.numel_padded, dtype=torch.float32, device=device)
+        self.grad: Optional[torch.Tensor] = (
+            None if zero_stage >= 3 else torch.zeros(self.numel_padded, dtype=torch.float32, device=device)
+        )
+        self.grad_shard: Optional[torch.Tensor] = (
+            torch.zeros(self.shard_size, dtype=torch.float32, device=device) if zero_stage >= 2 else None
+        )
+        self._offsets: List[Tuple[int, nn.Parameter]] = list(zip(lay.offsets, self.params))
+        self._numels: List[int] = list(lay.numels)
+        self._shapes: List[Tuple[int, ...]] = [tuple(p.shape) for p in self.params]
+        self._partitioned = False
+        # True while `grad` / `grad_shard` may hold non-zero values; lets
+        # zero_grad skip clearing buffers the fused boundary never wrote.
+        self._grad_dirty = False
+        self._tables = {}
+
+    # ------------------------------------------------------------- ranges
+    @property
+    def master_range(self) -> Range:
+        if self._partitioned:
+            return self.shard_start, self.shard_end
+        return 0, self.numel_padded
+
+    @property
+    def own_range(self) -> Range:
+        return self.shard_start, self.shard_end
+
+    def _pdata_range(self, offset: int, n: int, p: nn.Parameter) -> Range:
+        """Flat range covered by ``p.data``: the whole parameter, or the
+        owned slice of a ZeRO-3 placeholder (flat.py:103-113)."""
+        if p.data.numel() == n:
+            return offset, offset + n
+        start = max(offset, self.shard_start)
+        return start, start + p.data.numel()
+
+    def model_dtype(self) -> torch.dtype:
+        dtypes = {p.dtype for p in self.params}
+        if len(dtypes) != 1:
+            raise TypeError(f"parameters of one group must share a dtype, got {sorted(map(str, dtypes))}")
+        return next(iter(dtypes))
+
+    def table(self, key: str) -> SegmentTable:
+        t = self._tables.get(key)
+        if t is None:
+            t = self._tables[key] = SegmentTable(self.device)
+        return t
+
+    def _storage(self, t: torch.Tensor, rng: Range):
+        _native.require_hip_tensor(t, "parameter storage")
+        return (t.data_ptr(), rng, t.element_size())
+
+    def model_storages(self) -> List[Optional[tuple]]:
+        out = []
+        for (offset, p), n in zip(self._offsets, self._numels):
+            d = p.data
+            if not d.is_contiguous():
+                raise RuntimeError("parameter data must be contiguous")
+            out.append(self._storage(d, self._pdata_range(offset, n, p)))
+        return out
+
+    # -------------------------------------------------------- conversions
+    @torch.no_grad()
+    def copy_model_to_flat(self) -> None:
+        """Snapshot the parameters covered by ``master_range`` into ``data``
+        (flat.py:115-131): a ragged widening copy on the GPU."""
+        ms, me = self.master_range
+        dtype = self.model_dtype()
+        stores = self.model_storages()
+        table = self.layout.segments(ms, me, stores, [None] * len(stores))
+        check_table(table, ms, me)
+        ptr, n = self.table("to_flat").upload(table)
+        lib = _native.load()
+        rc = lib.ms_grad_stats(
+            ptr, n, _native.ms_dtype(dtype), ms, me, ms, me, 0, 1.0,
+            self.data.data_ptr(), None, None, 0, _native.stream_handle(self.device),
+        )
+        _native.check(rc, "ms_grad_stats(flatten)")
+
+    @torch.no_grad()
+    def copy_flat_to_model(self, full_flat: Optional[torch.Tensor] = None) -> None:
+        """Cast fp32 masters into the covered parameter elements
+        (flat.py:133-154): ``full_flat`` covers ``[0, numel_padded)``; by
+        default ``data`` over ``master_range`` is used."""
+        if full_flat is not None:
+            buf, base = full_flat, 0
+        else:
+            buf, base = self.data, self.master_range[0]
+        _native.require_hip_tensor(buf, "flat master buffer")
+        end = base + buf.numel()
+        dtype = self.model_dtype()
+        stores = self.model_storages()
+        table = self.layout.segments(base, end, [None] * len(stores), stores)
+        check_table(table, base, end)
+        ptr, n = self.table("to_model").upload(table)
+        rc = _native.load().ms_cast_to_model(
+            buf.data_ptr(), base, end, ptr, n, _native.ms_dtype(dtype),
+            _native.stream_handle(self.device),
+        )
+        _native.check(rc, "ms_cast_to_model")
+
+    # ---------------------------------------------------- stage-3 params
+    @torch.no_grad()
+    def partition_params(self) -> None:
+        """Keep only the owned master shard; parameters become flat
+        placeholders of their owned slices (flat.py:157-172)."""
+        if self._partitioned:
+            return
+        self.data = self.data[self.shard_start:self.shard_end].clone()
+        self._partitioned = True
+        self.dematerialize_params()
+        self.copy_flat_to_model()
+
+    @torch.no_grad()
+    def materialize_params(self) -> None:
+        if not self._partitioned:
+            return
+        for p, shape in zip(self.params, self._shapes):
+            p.data = torch.empty(shape, dtype=p.data.dtype, device=p.data.device)
+
+    @torch.no_grad()
+    def dematerialize_params(self) -> None:
+        if not self._partitioned:
+            return
+        for (offset, p), n in zip(self._offsets, self._numels):
+            lo, hi = _overlap((offset, offset + n), (self.shard_start, self.shard_end))
+            p.data = torch.empty(max(0, hi - lo), dtype=p.data.dtype, device=p.data.device)
+
+    # ----------------------------------------------------------- grads
+    def grad_storages(self) -> Tuple[List[Optional[tuple]], List[torch.Tensor]]:
+        """Ragged gradient storage of every parameter, in group order.
+
+        Returns the storage descriptors and the tensors they point into (the
+        caller keeps those alive until the kernels reading them have run).
+        """
+        stores: List[Optional[tuple]] = []
+        keep: List[torch.Tensor] = []
+        dtype = self.model_dtype()
+        for (offset, p), n in zip(self._offsets, self._numels):
+            g = p.grad
+            if g is None:
+                stores.append(None)
+                continue
+            if g.numel() != n:
+                raise RuntimeError(
+                    f"gradient of a parameter has {g.numel()} elements, expected {n}"
+                )
+            if g.dtype != dtype:
+                raise TypeError(f"gradient dtype {g.dtype} differs from parameter dtype {dtype}")
+            g = _flat_view(g.detach())
+            keep.append(g)
+            stores.append(self._storage(g, (offset, offset + n)))
+        return stores, keep
+
+    def release_grads(self) -> None:
+        for p in self.params:
+            p.grad = None
+
+    @torch.no_grad()
+    def flatten_grads(self) -> None:
+        """``param.grad`` -> fp32 flat ``grad`` (flat.py:196-213); params
+        without a gradient contribute zeros, ``param.grad`` is released."""
+        if self.grad is None:
+            self.grad = torch.empty(self.numel_padded, dtype=torch.float32, device=self.device)
+        stores, keep = self.grad_storages()
+        table = self.layout.segments(0, self.numel_padded, stores, [None] * len(stores))
+        check_table(table, 0, self.numel_padded)
+        ptr, n = self.table("flatten").upload(table)
+        rc = _native.load().ms_grad_stats(
+            ptr, n, _native.ms_dtype(self.model_dtype()), 0, self.numel_padded, 0, 0, 0, 1.0,
+            self.grad.data_ptr(), None, None, 0, _native.stream_handle(self.device),
+        )
+        _native.check(rc, "ms_grad_stats(flatten)")
+        self._grad_dirty = True
+        self.release_grads()
+        del keep  # stream order keeps the storage valid for the launched kernel
+
+    @torch.no_grad()
+    def zero_grad(self) -> None:
+        """flat.py:215-223; buffers the fused boundary never wrote are
+        already zero and are not cleared again."""
+        if self.grad is not None:
+            if self.zero_stage >= 3:
+                self.grad = None
+            elif self._grad_dirty:
+                self.grad.zero_()
+        if self.grad_shard is not None and self._grad_dirty:
+            self.grad_shard.zero_()
+        self._grad_dirty = False
+
+    def grad_for_shard(self) -> torch.Tensor:
+        if self.grad_shard is not None:
+            return self.grad_shard
+        return self.grad[self.shard_start:self.shard_end]
+
+    @property
+    def shard(self) -> torch.Tensor:
+        if self._partitioned:
+            return self.data
+        return self.data[self.shard_start:self.shard_end]
+
+    def numel_shard(self) -> int:
+        return self.shard_end - self.shard_start
+
+
+def build_flat_groups(
+    param_groups: Iterable[dict],
+    *,
+    rank: int,
+    world_size: int,
+    zero_stage: int,
+    device: torch.device,
+) -> Tuple[List[FlatParamGroup], List[dict]]:
+    """torch-style group dicts -> FlatParamGroups + option dicts
+    (flat.py:263-291)."""
+    flat_groups: List[FlatParamGroup] = []
+    option_groups: List[dict] = []
+    for group in param_groups:
+        params = [p for p in group["params"] if p.requires_grad]
+        if not params:
+            continue
+        flat_groups.append(
+            FlatParamGroup(params, rank=rank, world_size=world_size, zero_stage=zero_stage, device=device)
+        )
+        option_groups.append({k: v for k, v in group.items() if k != "params"})
+    if not flat_groups:
+        raise ValueError("No trainable parameters found")
+    return flat_groups, option_groups

@@ -1,0 +1,142 @@
+"""ZeRO stages 0/1/2 on one GPU (minispeed/zero/stage_1_and_2.py).
+
+At world size 1 the stages differ only in which flat buffers exist: stage 0
+and 1 are identical (the all-gather after the step is skipped, reference
+stage_1_and_2.py:139-145), stage 2 adds the ``grad_shard`` buffer that the
+world-1 reduce-scatter would copy into (stage_1_and_2.py:95-96).  The
+boundary step is the fused K1 -> K2 -> K3 sequence of ``boundary.py``; the
+fused path never materialises the flat gradient, so ``grad`` and
+``grad_shard`` stay the zeros the reference leaves in them after its
+``zero_grad``.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+
+from .. import comm
+from ..boundary import GroupLaunch, Workspace, run_boundary
+from ..flat import FlatParamGroup
+from ..optim.adam import FlatAdam
+
+
+class ZeROOptimizer:
+    def __init__(self, flat_groups: List[FlatParamGroup], option_groups: List[dict], zero_stage: int = 0):
+        if zero_stage not in (0, 1, 2, 3):
+            raise ValueError(f"Unsupported ZeRO stage: {zero_stage}")
+        self.flat_groups = flat_groups
+        self.zero_stage = zero_stage
+        self.world_size = comm.get_world_size()
+        self.rank = comm.get_rank()
+        self.adam = FlatAdam(flat_groups, option_groups, zero_stage=zero_stage)
+        self.grad_norm: Optional[float] = None
+        self._workspace: Optional[Workspace] = None
+
+    # ------------------------------------------------------ torch-ish surface
+    @property
+    def param_groups(self) -> List[dict]:
+        return self.adam.param_groups
+
+    @property
+    def state(self) -> List[dict]:
+        return self.adam.state
+
+    def zero_grad(self) -> None:
+        for g in self.flat_groups:
+            g.zero_grad()
+
+    # --------------------------------------------- parameter materialization
+    @property
+    def params_gathered(self) -> bool:
+        return True
+
+    @torch.no_grad()
+    def gather_parameters(self) -> None:
+        """Stages 0-2 keep full parameters resident."""
+
+    @torch.no_grad()
+    def free_parameters(self) -> None:
+        """Stages 0-2 keep full parameters resident."""
+
+    @torch.no_grad()
+    def sync_parameters(self) -> None:
+        """Cast the masters into the model parameters (stage_1_and_2.py:79-83)."""
+        for g in self.flat_groups:
+            g.copy_flat_to_model()
+
+    @torch.no_grad()
+    def step(self) -> bool:
+        """Unfused AdamW over already reduced/clipped grads (the reference's
+        ``ZeROOptimizer.step``); the engine uses :meth:`boundary_step`."""
+        return self.adam.step()
+
+    # ------------------------------------------------------ fused boundary
+    def _ws(self) -> Workspace:
+        if self._workspace is None:
+            self._workspace = Workspace(self.flat_groups[0].device, len(self.flat_groups))
+        return self._workspace
+
+    def _model_targets(self) -> List[Optional[List[Optional[tuple]]]]:
+        """Where K3 writes the model-dtype copy of each group."""
+        return [g.model_storages() for g in self.flat_groups]
+
+    def _after_boundary(self, overflow: bool) -> None:
+        """Stage-specific follow-up once the scalars are on the host."""
+
+    @torch.no_grad()
+    def boundary_step(self, scaler, max_norm: Optional[float], materialize_flat_grad: bool = False):
+        """Run flatten/flag/unscale/norm/clip/AdamW/cast for every group as
+        K1 -> K2 -> K3 and return the host copy of K2's scalars.
+
+        ``param.grad`` is released for every parameter (flat.py:213).  The
+        Adam step counters advance only for an applied step (the caller
+        commits them via :meth:`commit_step`).
+        """
+        ws = self._ws()
+        keep: List[torch.Tensor] = []
+        grads = []
+        for g in self.flat_groups:
+            stores, tensors = g.grad_storages()
+            grads.append(stores)
+            keep.extend(tensors)
+            g.release_grads()
+        models = self._model_targets()
+        launches = []
+        for g, group, state, gstores, mstores in zip(
+            self.flat_groups, self.adam.param_groups, self.adam.state, grads, models
+        ):
+            lr, betas, eps, wd = FlatAdam.hyper(group)
+            launches.append(GroupLaunch(
+                group=g, lr=lr, betas=betas, eps=eps, weight_decay=wd,
+                step=state["step"] + 1, exp_avg=state["exp_avg"], exp_avg_sq=state["exp_avg_sq"],
+                grads=gstores, model=mstores,
+            ))
+        scalars = run_boundary(
+            launches, ws, scaler=scaler, max_norm=max_norm,
+            materialize_flat_grad=materialize_flat_grad,
+        )
+        del keep  # the read-back synchronised the stream
+        overflow = bool(scalars.overflow)
+        if not overflow:
+            self.grad_norm = float(scalars.norm)
+        self._after_boundary(overflow)
+        return scalars
+
+    def commit_step(self) -> None:
+        """Advance every group's Adam step counter after an applied update
+        (adam.py:86)."""
+        for st in self.adam.state:
+            st["step"] += 1
+
+    # ---------------------------------------------------------- persistence
+    def state_dict(self) -> dict:
+        return self.adam.state_dict()
+
+    def load_state_dict(self, state: dict) -> None:
+        self.adam.load_state_dict(state)
+
+    def _grad_device(self) -> torch.device:
+        return self.flat_groups[0].device
+

@@ -1,0 +1,290 @@
+"""Kernel parity through the C ABI: K1 (ragged scan), K2 (norm / clip /
+skip / scale), K3 (fused AdamW + cast), K4 (cast) against the oracle.
+
+Bars: flat grads, flags, casts, scaler decisions and the fused AdamW against
+the kernel recipe (oracle.recipe) are bit-exact; the per-block fp64 sum of
+squares agrees with an exact fp64 dot product to 1e-12 relative; AdamW
+against the torch restatement (oracle.boundary) is bit-exact in exp_avg /
+exp_avg_sq and within 2 fp32 ulp of max(|p_old|, |p_new|) in the master,
+the only difference being torch's CPU sqrt.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from minispeed_amd import _native
+from oracle import boundary as ob
+from oracle import recipe
+from tests.helpers import (DEV, HALF_SPECIALS, Table, adamw_params, bits, k1, k2, k3, k4,
+                           layout_for, ragged_grads, scalars_device, set_bits, store)
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
+RAGGED = [(7, 5), (3,), (3 * 2048,), (1,), (4099,), (64, 65), (10000,)]
+ALIGNED = [(4096, 8), (8,), (5 * 2048,), (2048, 24)]
+
+
+def _oracle_flat(shapes, grads, scale):
+    dtype = next(g.dtype for g in grads if g is not None)
+    params = [nn.Parameter(torch.zeros(*s, dtype=dtype)) for s in shapes]
+    g = ob.Group(params)
+    for p, gr in zip(params, grads):
+        p.grad = None if gr is None else gr.clone()
+    g.flatten_grads()
+    flag = ob.has_overflow(g.grad)
+    g.unscale_grads(scale)
+    return g.grad, flag
+
+
+def _device(grads):
+    return [None if g is None else g.to(DEV) for g in grads]
+
+
+def _grad_table(shapes, dgrads, world=1, rank=0, stage=0, lo=None, hi=None):
+    lay = layout_for([int(np.prod(s)) for s in shapes], world, rank, stage)
+    lo = 0 if lo is None else lo
+    hi = lay.numel_padded if hi is None else hi
+    gs = [store(g, off) for g, off in zip(dgrads, lay.offsets)]
+    return lay, Table(lay, lo, hi, gs, [None] * len(shapes))
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+@pytest.mark.parametrize("scale", [1.0, 65536.0, 1000.0])
+@pytest.mark.parametrize("shapes", [RAGGED, ALIGNED], ids=["ragged", "aligned"])
+def test_k1_flatten_unscale_and_sumsq(dtype, scale, shapes):
+    grads = ragged_grads(shapes, dtype, 1e-3, seed=11, scale=scale if dtype == F16 else 1.0)
+    grads[1] = None                                   # a parameter without gradient
+    dg = _device(grads)
+    lay, tab = _grad_table(shapes, dg)
+    n = lay.numel_padded
+    flat = torch.full((n,), float("nan"), device=DEV)
+    psum, pflag = k1(tab, dtype, 0, n, 0, n, scale=scale, flat=flat)
+    want, flag = _oracle_flat(shapes, grads, scale)
+    assert not flag and not pflag.any()
+    np.testing.assert_array_equal(bits(flat), bits(want))
+    exact = recipe.sumsq_f64(want.numpy())
+    assert abs(psum.sum() - exact) <= 1e-12 * exact
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+def test_k1_flag_every_special_encoding(dtype):
+    shapes = RAGGED
+    specials = HALF_SPECIALS[dtype]
+    for k, pattern in enumerate(specials):
+        grads = ragged_grads(shapes, dtype, 1e-3, seed=20 + k)
+        # put the special in a different parameter / position each time
+        pi = [0, 2, 4, 5, 6, 3, 2, 6, 0][k]
+        idx = [3, 2047, 4098, 4159, 9999, 0, 5000, 1, 34][k]
+        set_bits(grads[pi], idx, pattern)
+        dg = _device(grads)
+        lay, tab = _grad_table(shapes, dg)
+        n = lay.numel_padded
+        psum, pflag = k1(tab, dtype, 0, n, 0, n)
+        _, want = _oracle_flat(shapes, grads, 1.0)
+        assert bool(pflag.any()) == want == (k < 5), (hex(pattern), pi, idx)
+        s = k2(psum, pflag)
+        assert bool(s.overflow) == want
+
+
+def test_k1_partials_are_deterministic():
+    shapes = ALIGNED + RAGGED
+    grads = _device(ragged_grads(shapes, BF16, 1e-2, seed=3))
+    lay, tab = _grad_table(shapes, grads)
+    n = lay.numel_padded
+    a = k1(tab, BF16, 0, n, 0, n)[0]
+    b = k1(tab, BF16, 0, n, 0, n)[0]
+    np.testing.assert_array_equal(a.view(np.int64), b.view(np.int64))
+
+
+def test_k1_owned_range_only_counts_owned_elements():
+    shapes = RAGGED
+    grads = ragged_grads(shapes, F32, 1e-2, seed=5)
+    dg = _device(grads)
+    lay, tab = _grad_table(shapes, dg, world=3, rank=1, stage=2)
+    n = lay.numel_padded
+    lo, hi = lay.shard_start, lay.shard_end
+    psum, _ = k1(tab, F32, 0, n, lo, hi)
+    flat, _ = _oracle_flat(shapes, grads, 1.0)
+    exact = recipe.sumsq_f64(flat.numpy()[lo:hi])
+    assert abs(psum.sum() - exact) <= 1e-12 * exact
+
+
+def test_k2_norm_clip_and_scaler_decisions():
+    nb = _native.stats_blocks()
+    rng = np.random.default_rng(0)
+    psum = rng.random(2 * nb) * 1e-3
+    pflag = np.zeros(2 * nb, dtype=np.int32)
+    g0 = np.float32(psum[:nb].sum())
+    g1 = np.float32(psum[nb:].sum())
+    want_sumsq = np.float32(g0 + g1)
+    s = k2(psum, pflag, ngroups=2, has_clip=True, max_norm=0.5,
+           scaler=(True, 2.0 ** 16, 998, 3, 1000, 1.0, 2.0 ** 24))
+    assert abs(int(np.float32(s.sumsq).view(np.int32)) - int(want_sumsq.view(np.int32))) <= 1
+    assert np.float32(s.norm) == np.sqrt(np.float32(s.sumsq))
+    applied, coef64, coef32 = recipe.clip_coef(s.norm, 0.5)
+    assert bool(s.clip_applied) == applied
+    assert s.coef64 == coef64 and np.float32(s.coef) == np.float32(coef32)
+    assert (s.next_scale, s.next_good_steps, s.next_skipped_steps) == (2.0 ** 16, 999, 3)
+    s = k2(psum, pflag, ngroups=2, scaler=(True, 2.0 ** 16, 999, 3, 1000, 1.0, 2.0 ** 24))
+    assert (s.next_scale, s.next_good_steps) == (2.0 ** 17, 0)
+    assert not s.clip_applied
+    s = k2(psum, pflag, ngroups=2, scaler=(True, 2.0 ** 24, 999, 3, 1000, 1.0, 2.0 ** 24))
+    assert (s.next_scale, s.next_good_steps) == (2.0 ** 24, 1000)
+    pflag[nb + 17] = 1
+    s = k2(psum, pflag, ngroups=2, has_clip=True, max_norm=1e-9,
+           scaler=(True, 1.0, 5, 3, 1000, 1.0, 2.0 ** 24))
+    assert s.overflow and not s.clip_applied
+    assert (s.next_scale, s.next_good_steps, s.next_skipped_steps) == (1.0, 0, 4)
+    s = k2(psum, pflag, ngroups=1)   # the flag sits in group 1 only
+    assert not s.overflow
+
+
+def _adam_case(shapes, gdtype, seed, scale=1.0, zero_grad_params=()):
+    rng = np.random.default_rng(seed)
+    lay = layout_for([int(np.prod(s)) for s in shapes])
+    n = lay.numel_padded
+    p = rng.normal(0, 0.02, n).astype(np.float32)
+    m = (rng.normal(0, 1e-3, n)).astype(np.float32)
+    v = (rng.random(n) * 1e-6).astype(np.float32)
+    grads = ragged_grads(shapes, gdtype, 1e-3, seed=seed + 1, scale=scale)
+    for i in zero_grad_params:
+        grads[i] = None
+    return lay, p, m, v, grads
+
+
+def _flat_np(lay, grads):
+    out = np.zeros(lay.numel_padded, dtype=np.float32)
+    for g, off in zip(grads, lay.offsets):
+        if g is not None:
+            out[off:off + g.numel()] = g.float().reshape(-1).numpy()
+    return out
+
+
+@pytest.mark.parametrize("gdtype", [F16, BF16, F32])
+@pytest.mark.parametrize("shapes", [RAGGED, ALIGNED], ids=["ragged", "aligned"])
+@pytest.mark.parametrize("variant", ["plain", "unscale_clip_decay", "flat_grad", "late_step"])
+def test_k3_matches_kernel_recipe_bitwise(gdtype, shapes, variant):
+    scale = 65536.0 if variant == "unscale_clip_decay" and gdtype == F16 else 1.0
+    lay, p, m, v, grads = _adam_case(shapes, gdtype, seed=7, scale=scale, zero_grad_params=(1,))
+    n = lay.numel_padded
+    lr, betas, eps = 1e-3, (0.9, 0.999), 1e-8
+    wd = 0.01 if variant in ("unscale_clip_decay", "late_step") else 0.0
+    step = 1000 if variant == "late_step" else 3
+    clip = 0.37 if variant in ("unscale_clip_decay", "late_step") else None
+    dg = _device(grads)
+    models = [torch.zeros(s, dtype=gdtype, device=DEV) for s in shapes]
+    gst = [store(g, off) for g, off in zip(dg, lay.offsets)]
+    mst = [store(t, off) for t, off in zip(models, lay.offsets)]
+    flat_grad = None
+    unscale = scale != 1.0
+    if variant == "flat_grad":
+        flat_grad = torch.from_numpy(_flat_np(lay, grads)).to(DEV)
+        tab = Table(lay, 0, n, [None] * len(shapes), mst)
+    else:
+        tab = Table(lay, 0, n, gst, mst)
+    dp, dm, dv = (torch.from_numpy(x.copy()).to(DEV) for x in (p, m, v))
+    hp = adamw_params(lr, betas, eps, wd, step, grad_scale=scale, unscale=unscale)
+    sc = scalars_device(clip_applied=1 if clip else 0, coef=clip or 1.0)
+    k3(tab, gdtype, gdtype, 0, n, dp, dm, dv, hp, sc, flat_grad=flat_grad)
+    g = _flat_np(lay, grads)
+    wp, wm, wv = recipe.adamw_step(p, m, v, g, lr=lr, betas=betas, eps=eps, wd=wd, step=step,
+                                   grad_scale=scale, unscale=unscale, clip_coef=clip)
+    np.testing.assert_array_equal(dm.cpu().numpy().view(np.int32), wm.view(np.int32))
+    np.testing.assert_array_equal(dv.cpu().numpy().view(np.int32), wv.view(np.int32))
+    np.testing.assert_array_equal(dp.cpu().numpy().view(np.int32), wp.view(np.int32))
+    want_model = torch.from_numpy(wp).to(gdtype)
+    got_model = torch.cat([t.reshape(-1).cpu() for t in models])
+    np.testing.assert_array_equal(bits(got_model), bits(want_model[:lay.numel]))
+
+
+@pytest.mark.parametrize("gdtype", [F16, BF16])
+def test_k3_against_torch_restatement(gdtype):
+    shapes = RAGGED
+    lay, p, m, v, grads = _adam_case(shapes, gdtype, seed=9)
+    n = lay.numel_padded
+    lr, betas, eps, wd, step, coef = 1e-3, (0.9, 0.999), 1e-8, 0.01, 5, 0.41
+    dg = _device(grads)
+    tab = Table(lay, 0, n, [store(g, off) for g, off in zip(dg, lay.offsets)], [None] * len(shapes))
+    dp, dm, dv = (torch.from_numpy(x.copy()).to(DEV) for x in (p, m, v))
+    k3(tab, gdtype, gdtype, 0, n, dp, dm, dv, adamw_params(lr, betas, eps, wd, step),
+       scalars_device(clip_applied=1, coef=coef))
+    tp, tm, tv = (torch.from_numpy(x.copy()) for x in (p, m, v))
+    tg = torch.from_numpy(_flat_np(lay, grads))
+    tg.mul_(float(np.float32(coef)))
+    ob.adam_update(tp, tg, tm, tv, lr, betas, eps, wd, step)
+    np.testing.assert_array_equal(dm.cpu().numpy(), tm.numpy())
+    np.testing.assert_array_equal(dv.cpu().numpy(), tv.numpy())
+    got = dp.cpu().numpy()
+    scale = np.maximum(np.abs(p), np.abs(tp.numpy()))
+    assert np.all(np.abs(got.astype(np.float64) - tp.numpy()) <= 2 * np.spacing(scale))
+
+
+def test_k3_skips_everything_on_overflow():
+    shapes = RAGGED
+    lay, p, m, v, grads = _adam_case(shapes, F16, seed=2)
+    n = lay.numel_padded
+    dg = _device(grads)
+    models = [torch.full(s, 7.0, dtype=F16, device=DEV) for s in shapes]
+    tab = Table(lay, 0, n, [store(g, off) for g, off in zip(dg, lay.offsets)],
+                [store(t, off) for t, off in zip(models, lay.offsets)])
+    dp, dm, dv = (torch.from_numpy(x.copy()).to(DEV) for x in (p, m, v))
+    k3(tab, F16, F16, 0, n, dp, dm, dv, adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 1),
+       scalars_device(overflow=1))
+    np.testing.assert_array_equal(dp.cpu().numpy(), p)
+    np.testing.assert_array_equal(dm.cpu().numpy(), m)
+    np.testing.assert_array_equal(dv.cpu().numpy(), v)
+    assert all(bool((t == 7.0).all()) for t in models)
+
+
+def test_k3_shard_range_with_placeholders():
+    """Rank 1 of 3 (ZeRO-3 style): masters/moments hold the owned slice only
+    and every model destination is a placeholder of that slice."""
+    shapes = RAGGED
+    numels = [int(np.prod(s)) for s in shapes]
+    lay = layout_for(numels, world_size=3, rank=1, stage=3)
+    lo, hi = lay.shard_start, lay.shard_end
+    rng = np.random.default_rng(4)
+    p = rng.normal(0, 0.02, hi - lo).astype(np.float32)
+    m = np.zeros(hi - lo, np.float32)
+    v = np.zeros(hi - lo, np.float32)
+    grads = ragged_grads(shapes, BF16, 1e-3, seed=8)
+    dg = _device(grads)
+    holders, mst = [], []
+    for off, nn_ in zip(lay.offsets, numels):
+        a, b = max(off, lo), min(off + nn_, hi)
+        t = torch.zeros(max(0, b - a), dtype=BF16, device=DEV)
+        holders.append((a, b, t))
+        mst.append((t.data_ptr(), (a, b), 2) if b > a else None)
+    tab = Table(lay, lo, hi, [store(g, off) for g, off in zip(dg, lay.offsets)], mst)
+    dp, dm, dv = (torch.from_numpy(x.copy()).to(DEV) for x in (p, m, v))
+    hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.0, 1)
+    k3(tab, BF16, BF16, lo, hi, dp, dm, dv, hp, scalars_device())
+    g = _flat_np(lay, grads)[lo:hi]
+    wp, _, _ = recipe.adamw_step(p, m, v, g, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, wd=0.0, step=1)
+    np.testing.assert_array_equal(dp.cpu().numpy().view(np.int32), wp.view(np.int32))
+    want = torch.from_numpy(wp).to(BF16)
+    for a, b, t in holders:
+        if b > a:
+            np.testing.assert_array_equal(bits(t), bits(want[a - lo:b - lo]))
+
+
+@pytest.mark.parametrize("mdtype", [F16, BF16, F32])
+def test_k4_cast_matches_torch_rounding(mdtype):
+    rng = np.random.default_rng(1)
+    shapes = RAGGED
+    lay = layout_for([int(np.prod(s)) for s in shapes])
+    n = lay.numel_padded
+    flat = (rng.normal(0, 1, n) * np.exp(rng.uniform(-30, 30, n))).astype(np.float32)
+    flat[:6] = [65519.0, 65520.0, -1e5, 1e-8, -0.0, 3.0e38]
+    flat[6:9] = np.array([1, 0x80001, 0x7F7FFFFF], dtype=np.int32).view(np.float32)
+    models = [torch.zeros(s, dtype=mdtype, device=DEV) for s in shapes]
+    tab = Table(lay, 0, n, [None] * len(shapes), [store(t, off) for t, off in zip(models, lay.offsets)])
+    k4(tab, mdtype, torch.from_numpy(flat).to(DEV), 0, n)
+    want = torch.from_numpy(flat[:lay.numel]).to(mdtype)
+    got = torch.cat([t.reshape(-1).cpu() for t in models])
+    np.testing.assert_array_equal(bits(got), bits(want))
