@@ -1,0 +1,282 @@
+"""Boundary-step throughput of minispeed_amd on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload gpt-1.3b]
+                    [--grad-dtype fp16] [--mode fused|materialize]
+                    [--no-cpu-baseline] [--copy-calibration]
+
+A step is one gradient-accumulation boundary through the engine API
+(``engine.step()``): the ragged-grad scan, the norm/clip/skip decision and
+the fused AdamW + model cast, plus the one read-back of the step scalars and
+the host bookkeeping.  The gradients are resident in HBM before the timed
+region (each step re-attaches one of two pre-generated gradient sets to
+``param.grad``, which is what the last ``backward`` of a window leaves).
+
+Workload (default): the 1.3B GPT-style buffer (24 layers, d 2048, vocab
+50257, 292 ragged tensors, 1,315,723,264 params), fp16 gradients
+N(0,1e-3) x 2^16 under the dynamic loss scale 2^16, fp32 masters N(0,0.02),
+ZeRO-1 at world size 1, clip 1.0, AdamW (lr 1e-3, betas 0.9/0.999, eps 1e-8,
+wd 0.01), WarmupDecayLR 100/1000.
+
+Printed: one JSON line with Gparams/s as ``value``, whole-step HBM GB/s at
+the algorithmic bytes per parameter, the dominant kernel's roofline (K3,
+timed with HIP events on its own stream over the timed steps) and the CPU
+baseline (the oracle's torch restatement of the reference step on this
+host's cores, on a bounded sample of the same tensor list).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "boundary-step Gparams/s + HBM GB/s (% of peak) at 1.3B fp16, 1 GPU"
+PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+# algorithmic bytes per parameter: (K1, K3) for half / fp32 gradients
+BYTES = {
+    ("fused", 2): (2, 28),         # K1 read g2 | K3 read g2+p4+m4+v4, write p4+m4+v4+model2
+    ("materialize", 2): (6, 30),   # K1 read g2 write f4 | K3 read f4+12, write 12+2
+    ("fused", 4): (4, 32),
+    ("materialize", 4): (8, 32),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="gpt-1.3b")
+    ap.add_argument("--grad-dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
+    ap.add_argument("--mode", default="fused", choices=["fused", "materialize"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-params", type=int, default=50_000_000)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (a counter yardstick for rocprofv3 --pmc)")
+    return ap.parse_args(argv)
+
+
+def engine_config(grad_dtype: str, mode: str) -> dict:
+    cfg = {
+        "train_micro_batch_size_per_gpu": 1,
+        "gradient_accumulation_steps": 1,
+        "gradient_clipping": 1.0,
+        "dtype": grad_dtype,
+        "optimizer": {"type": "AdamW",
+                      "params": {"lr": 1e-3, "betas": [0.9, 0.999], "eps": 1e-8, "weight_decay": 0.01}},
+        "scheduler": {"type": "WarmupDecayLR",
+                      "params": {"warmup_min_lr": 0.0, "warmup_max_lr": 1e-3,
+                                 "warmup_num_steps": 100, "total_num_steps": 1000}},
+        "zero_optimization": {"stage": 1},
+        "hip_boundary": {"materialize_flat_grad": mode == "materialize"},
+        "steps_per_print": 1000000,
+    }
+    if grad_dtype == "fp16":
+        cfg["fp16"] = {"enabled": True, "loss_scale": 0, "initial_scale_power": 16,
+                       "loss_scale_window": 1000}
+    return cfg
+
+
+def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
+    """Time the oracle's torch restatement of the reference boundary step on
+    the host cores over the leading tensors of the same list."""
+    import torch
+    from torch import nn
+
+    from oracle import boundary as ob
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    threads = max(1, min(threads, 16))
+    torch.set_num_threads(threads)
+    # whole transformer layers after the embeddings, until the sample size
+    sample, total = [], 0
+    for s in shapes[2:]:
+        if total >= sample_params:
+            break
+        n = 1
+        for x in s:
+            n *= x
+        sample.append(s)
+        total += n
+    gen = torch.Generator().manual_seed(0)
+    params = [nn.Parameter(torch.randn(*s, generator=gen) * 0.02) for s in sample]
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[grad_dtype]
+    eng = ob.Engine([params], [{"lr": 1e-3, "weight_decay": 0.01}], dtype=grad_dtype, zero_stage=1,
+                    clip=1.0, initial_scale_power=16, scheduler="WarmupDecayLR",
+                    scheduler_params={"warmup_max_lr": 1e-3, "warmup_num_steps": 100,
+                                      "total_num_steps": 1000})
+    mult = 2.0 ** 16 if grad_dtype == "fp16" else 1.0
+    grads = [(torch.randn(*s, generator=gen) * 1e-3 * mult).to(dt) for s in sample]
+    times = []
+    for it in range(4):
+        for p, g in zip(params, grads):
+            p.grad = g
+        eng.micro_steps += 1
+        t0 = time.perf_counter()
+        ok = eng.step()
+        times.append(time.perf_counter() - t0)
+        assert ok
+    times = sorted(times[1:])
+    med = times[len(times) // 2]
+    return {
+        "value": total / med / 1e9,
+        "unit": "Gparams/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle torch-CPU restatement of the reference step on {len(sample)} tensors "
+                   f"({total:,} params: the leading transformer layers of the same list); "
+                   f"median of 3 steps after 1 warm-up, "
+                   f"{med * 1e3:.0f} ms/step"),
+    }
+
+
+def traffic_for(kernel: str, workload: str, grad_dtype: str, mode: str):
+    """HBM bytes per launch measured by rocprofv3 counters (profiles/traffic.json)."""
+    try:
+        with open(TRAFFIC_FILE, "r", encoding="utf-8") as fh:
+            table = json.load(fh)
+    except OSError:
+        return None
+    entry = table.get(f"{kernel}/{workload}/{grad_dtype}/{mode}")
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
+def main(argv=None) -> int:
+    args = parse(argv)
+    if args.gpus != 1:
+        print(json.dumps({"error": f"--gpus {args.gpus}: this build measures the boundary step on one "
+                                   "GPU; multi-GPU runs are not part of it"}))
+        return 2
+    import numpy as np
+    import torch
+    from torch import nn
+
+    import minispeed_amd as ms
+    from minispeed_amd.boundary import LaunchTimer
+    from minispeed_amd.workloads import WORKLOADS, numel, shapes_of
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}))
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    shapes = shapes_of(args.workload)
+    n_params = numel(shapes)
+    gdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.grad_dtype]
+    log(f"[bench] workload {args.workload}: {len(shapes)} tensors, {n_params:,} params, "
+        f"grads {args.grad_dtype}, mode {args.mode}")
+
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    params = [nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
+    module = nn.ParameterList(params)
+    engine = ms.initialize(model=module, model_parameters=list(module),
+                           config=engine_config(args.grad_dtype, args.mode))
+    mult = 2.0 ** 16 if args.grad_dtype == "fp16" else 1.0
+    grad_sets = []
+    for _ in range(2):
+        grad_sets.append([(torch.randn(*s, generator=gen, device=dev) * (1e-3 * mult)).to(gdt)
+                          for s in shapes])
+    torch.cuda.synchronize()
+    log("[bench] buffers resident; warming up")
+
+    def one_step(k: int) -> None:
+        for p, g in zip(params, grad_sets[k % 2]):
+            p.grad = g
+        engine.micro_steps += 1          # what engine.backward counts
+        if not engine.step():
+            raise RuntimeError("boundary step was skipped (unexpected overflow)")
+
+    for k in range(args.warmup):
+        one_step(k)
+    torch.cuda.synchronize()
+    timer = LaunchTimer()
+    engine.optimizer.launch_timer = timer
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        one_step(k)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    engine.optimizer.launch_timer = None
+    log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev)   # 1 GiB
+        dst = torch.empty_like(src)
+        src.fill_(1.0)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] copy calibration: 3 x 1 GiB device copies (read 1 GiB + write 1 GiB each)")
+
+    ms_step = elapsed / args.steps * 1e3
+    esize = 4 if args.grad_dtype == "fp32" else 2
+    b1, b3 = BYTES[(args.mode, esize)]
+    k_ms = {k: float(np.mean(timer.durations_ms(k))) for k in ("k1", "k2", "k3")}
+    k3_gbps = b3 * n_params / (k_ms["k3"] * 1e-3) / 1e9
+    step_gbps = (b1 + b3) * n_params / (ms_step * 1e-3) / 1e9
+    traffic = traffic_for("k3", args.workload, args.grad_dtype, args.mode)
+    result = {
+        "metric": METRIC,
+        "value": round(n_params / (ms_step * 1e-3) / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": (f"synthetic: seeded {args.grad_dtype} grads N(0,1e-3)"
+                 + (" x 2^16" if args.grad_dtype == "fp16" else "") + ", fp32 masters N(0,0.02)"),
+        "config": {
+            "workload": WORKLOADS[args.workload]["desc"],
+            "params": n_params,
+            "tensors": len(shapes),
+            "grad_dtype": args.grad_dtype,
+            "model_dtype": args.grad_dtype,
+            "zero_stage": 1,
+            "world_size": 1,
+            "mode": args.mode,
+            "clip": 1.0,
+            "bytes_per_param": b1 + b3,
+        },
+        "hbm_gbps": round(step_gbps, 1),
+        "hbm_frac": round(step_gbps / PEAK_GBPS, 4),
+        "kernel_ms": {k: round(v, 4) for k, v in k_ms.items()},
+        "roofline": {
+            "kernel": "K3 k_adamw (fused AdamW + model cast)",
+            "bound": "hbm",
+            "achieved": round(k3_gbps, 1),
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(k3_gbps / PEAK_GBPS, 4),
+            "traffic": traffic,
+            "bytes_per_param": b3,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        del grad_sets, engine, params, module
+        torch.cuda.empty_cache()
+        log("[bench] CPU baseline (oracle restatement on host cores)")
+        result["cpu_baseline"] = cpu_baseline(shapes, args.grad_dtype, args.cpu_sample_params)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -89,6 +89,47 @@ class Workspace:
         return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
 
 
+class LaunchTimer:
+    """Optional HIP-event timing of the boundary kernels.
+
+    When attached to an optimizer (``optimizer.launch_timer``), every K1 /
+    K2 / K3 launch is bracketed by events recorded on the current stream,
+    the stream the kernels run on.  ``durations_ms(name)`` is valid after
+    the stream has been synchronised.
+    """
+
+    def __init__(self):
+        self._events = {}
+
+    def start(self, name: str):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return (name, ev)
+
+    def stop(self, token) -> None:
+        name, start = token
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        self._events.setdefault(name, []).append((start, end))
+
+    def durations_ms(self, name: str) -> List[float]:
+        return [a.elapsed_time(b) for a, b in self._events.get(name, [])]
+
+    def reset(self) -> None:
+        self._events.clear()
+
+
+class _NoTimer:
+    def start(self, name):
+        return None
+
+    def stop(self, token):
+        return None
+
+
+_NO_TIMER = _NoTimer()
+
+
 @dataclass
 class GroupLaunch:
     """What K1/K3 need for one group at one boundary."""
@@ -101,53 +142,24 @@ class GroupLaunch:
     step: int                     # Adam step number this update would use
     exp_avg: torch.Tensor         # owned-range moments (optim/adam.py:58-65)
     exp_avg_sq: torch.Tensor
-    grads: List[Optional[tuple]]            # ragged grad storages (FlatParamGroup.grad_storages)
-    model: Optional[List[Optional[tuple]]]  # model storages, None: no write
+    grads: List[int]              # gradient address per parameter (0: none)
+    model: Optional[List[int]]    # cast target per parameter, None: no write
 
 
-def _launch_k1(lib, ws: Workspace, gi: int, g: FlatParamGroup, grad_stores, dtype: int,
-               unscale: bool, scale: float, flat_out: Optional[torch.Tensor], stream: int) -> None:
-    n = g.numel_padded
-    table = g.layout.segments(0, n, grad_stores, [None] * len(grad_stores))
-    check_table(table, 0, n)
-    ptr, nseg = g.table("k1").upload(table)
-    psum, pflag = ws.partial_ptrs(gi)
-    lo, hi = g.own_range
-    rc = lib.ms_grad_stats(
-        ptr, nseg, dtype, 0, n, lo, hi, 1 if unscale else 0, _f32(scale),
-        flat_out.data_ptr() if flat_out is not None else None,
-        psum, pflag, ws.nblk, stream,
-    )
-    _native.check(rc, "ms_grad_stats")
+def _tables(gl: GroupLaunch):
+    """(K1 table over [0, N), K3 table over the owned range), uploaded.
 
-
-def _launch_k3(lib, ws: Workspace, gl: GroupLaunch, grad_stores, gdtype: int, mdtype: int,
-               unscale: bool, scale: float, flat_grad: Optional[torch.Tensor], stream: int) -> None:
+    At world size 1 both ranges are the whole padded space and one table
+    (gradient and model addresses) serves both kernels."""
     g = gl.group
     lo, hi = g.own_range
-    if hi <= lo:
-        return
-    models = gl.model if gl.model is not None else [None] * len(g.params)
-    grads = grad_stores if flat_grad is None else [None] * len(g.params)
-    table = g.layout.segments(lo, hi, grads, models)
-    check_table(table, lo, hi)
-    ptr, nseg = g.table("k3").upload(table)
-    hp = adamw_params(gl.lr, gl.betas, gl.eps, gl.weight_decay, gl.step,
-                      grad_scale=scale, unscale=unscale and flat_grad is None)
-    master = g.shard
-    if master.numel() != hi - lo or gl.exp_avg.numel() != hi - lo or gl.exp_avg_sq.numel() != hi - lo:
-        raise RuntimeError(
-            f"grad/shard shape mismatch: owned range {hi - lo} vs master {master.numel()}, "
-            f"moments {gl.exp_avg.numel()}/{gl.exp_avg_sq.numel()}"
-        )
-    fg_ptr = None
-    if flat_grad is not None:
-        fg_ptr = flat_grad.data_ptr() + lo * 4
-    rc = lib.ms_fused_adamw(
-        master.data_ptr(), gl.exp_avg.data_ptr(), gl.exp_avg_sq.data_ptr(), fg_ptr,
-        ptr, nseg, gdtype, mdtype, lo, hi, ctypes.byref(hp), ws.scalars.data_ptr(), stream,
-    )
-    _native.check(rc, "ms_fused_adamw")
+    if g.whole_range:
+        t = g.boundary_table(0, g.numel_padded, gl.grads, gl.model)
+        dev = g.table("boundary").upload(t)
+        return dev, dev
+    t1 = g.boundary_table(0, g.numel_padded, gl.grads, None)
+    t3 = g.boundary_table(lo, hi, gl.grads, gl.model)
+    return g.table("k1").upload(t1), g.table("k3").upload(t3)
 
 
 def run_boundary(
@@ -157,6 +169,7 @@ def run_boundary(
     scaler,
     max_norm: Optional[float],
     materialize_flat_grad: bool,
+    timer: Optional[LaunchTimer] = None,
 ) -> _native.StepScalars:
     """Launch the whole boundary and return K2's scalars (one host sync).
 
@@ -168,8 +181,10 @@ def run_boundary(
     stream = _native.stream_handle(device)
     scale = float(scaler.loss_scale_factor)
     unscale = scale != 1.0
+    scale32 = _f32(scale)
+    timer = timer or _NO_TIMER
 
-    per_group = []
+    prepared = []
     for gi, gl in enumerate(launches):
         g = gl.group
         dtype = _native.ms_dtype(g.model_dtype())
@@ -179,9 +194,32 @@ def run_boundary(
                 g.grad = torch.empty(g.numel_padded, dtype=torch.float32, device=device)
             flat_out = g.grad
             g._grad_dirty = True
-        _launch_k1(lib, ws, gi, g, gl.grads, dtype, unscale, scale, flat_out, stream)
-        per_group.append((dtype, flat_out))
+        lo, hi = g.own_range
+        master = g.shard
+        if master.numel() != hi - lo or gl.exp_avg.numel() != hi - lo or gl.exp_avg_sq.numel() != hi - lo:
+            raise RuntimeError(
+                f"grad/shard shape mismatch: owned range {hi - lo} vs master {master.numel()}, "
+                f"moments {gl.exp_avg.numel()}/{gl.exp_avg_sq.numel()}"
+            )
+        t1, t3 = _tables(gl)
+        hp = adamw_params(gl.lr, gl.betas, gl.eps, gl.weight_decay, gl.step,
+                          grad_scale=scale, unscale=unscale and flat_out is None)
+        prepared.append((gi, gl, dtype, flat_out, t1, t3, hp, master))
 
+    for gi, gl, dtype, flat_out, t1, t3, hp, master in prepared:
+        g = gl.group
+        lo, hi = g.own_range
+        psum, pflag = ws.partial_ptrs(gi)
+        tok = timer.start("k1")
+        rc = lib.ms_grad_stats(
+            t1[0], t1[1], dtype, 0, g.numel_padded, lo, hi, 1 if unscale else 0, scale32,
+            flat_out.data_ptr() if flat_out is not None else None,
+            psum, pflag, ws.nblk, stream,
+        )
+        timer.stop(tok)
+        _native.check(rc, "ms_grad_stats")
+
+    tok = timer.start("k2")
     rc = lib.ms_norm_clip(
         ws.partials.data_ptr(), ws.flags.data_ptr(), ws.nblk, len(launches),
         1 if max_norm is not None else 0, float(max_norm or 0.0),
@@ -190,10 +228,22 @@ def run_boundary(
         float(scaler.min_scale), float(scaler.max_scale),
         ws.scalars.data_ptr(), stream,
     )
+    timer.stop(tok)
     _native.check(rc, "ms_norm_clip")
 
-    for gl, (dtype, flat_out) in zip(launches, per_group):
-        _launch_k3(lib, ws, gl, gl.grads, dtype, dtype, unscale, scale, flat_out, stream)
+    for gi, gl, dtype, flat_out, t1, t3, hp, master in prepared:
+        g = gl.group
+        lo, hi = g.own_range
+        if hi <= lo:
+            continue
+        fg_ptr = flat_out.data_ptr() + lo * 4 if flat_out is not None else None
+        tok = timer.start("k3")
+        rc = lib.ms_fused_adamw(
+            master.data_ptr(), gl.exp_avg.data_ptr(), gl.exp_avg_sq.data_ptr(), fg_ptr,
+            t3[0], t3[1], dtype, dtype, lo, hi, ctypes.byref(hp), ws.scalars.data_ptr(), stream,
+        )
+        timer.stop(tok)
+        _native.check(rc, "ms_fused_adamw")
 
     return ws.read_scalars()
 

@@ -28,6 +28,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <math.h>
 #include <stdlib.h>
 
 #include "minispeed_boundary.h"
@@ -52,6 +53,10 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 struct DF32 {
   using raw = uint32_t;
   static constexpr int kBytes = 4;
+  // packed inf/nan test: ((w & kExp) + kExpOne) sets bit 31 exactly when
+  // the exponent field is all ones
+  static constexpr uint32_t kExp = 0x7f800000u, kExpOne = 0x00800000u,
+                            kTop = 0x80000000u;
   __device__ static float widen(raw r) { return __uint_as_float(r); }
   __device__ static bool nonfinite(raw r) {
     return (r & 0x7f800000u) == 0x7f800000u;
@@ -62,6 +67,10 @@ struct DF32 {
 struct DF16 {
   using raw = uint16_t;
   static constexpr int kBytes = 2;
+  // per 16-bit half: the add carries into the half's top bit exactly when
+  // its exponent field is all ones, and never into the next half
+  static constexpr uint32_t kExp = 0x7c007c00u, kExpOne = 0x04000400u,
+                            kTop = 0x80008000u;
   __device__ static float widen(raw r) {
     return static_cast<float>(__builtin_bit_cast(_Float16, r));
   }
@@ -74,6 +83,8 @@ struct DF16 {
 struct DBF16 {
   using raw = uint16_t;
   static constexpr int kBytes = 2;
+  static constexpr uint32_t kExp = 0x7f807f80u, kExpOne = 0x00800080u,
+                            kTop = 0x80008000u;
   __device__ static float widen(raw r) {
     return __uint_as_float(static_cast<uint32_t>(r) << 16);
   }
@@ -105,6 +116,26 @@ __device__ inline void load_raw8(const void* p, typename D::raw (&r)[kVec]) {
       r[4 + k] = b[k];
     }
   }
+}
+
+// kVec raw elements as 32-bit words (kVec*kBytes/4 of them), 16-byte aligned.
+template <class D>
+__device__ inline void load_words(const void* p, uint32_t (&w)[kVec * D::kBytes / 4]) {
+  const u4* q = reinterpret_cast<const u4*>(p);
+#pragma unroll
+  for (int j = 0; j < kVec * D::kBytes / 16; ++j) {
+    const u4 x = q[j];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[4 * j + k] = x[k];
+  }
+}
+
+template <class D>
+__device__ inline typename D::raw word_elem(const uint32_t (&w)[kVec * D::kBytes / 4], int k) {
+  if constexpr (D::kBytes == 2)
+    return static_cast<uint16_t>((k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu));
+  else
+    return w[k];
 }
 
 template <class D>
@@ -182,6 +213,15 @@ __device__ inline int64_t seg_end(const ms_segment_t& s) {
   return s.begin + s.numel;
 }
 
+// Loss-scale division.  mode 0: none; 1: multiply by the exact reciprocal of
+// a power-of-two scale (x / 2^k and x * 2^-k round identically, subnormal
+// results included); 2: IEEE division.
+__device__ inline float unscale1(float g, int mode, float scale, float inv) {
+  if (mode == 1) return g * inv;
+  if (mode == 2) return g / scale;
+  return g;
+}
+
 // ------------------------------------------------------- block reductions
 __device__ inline double wave_sum(double x) {
 #pragma unroll
@@ -190,84 +230,129 @@ __device__ inline double wave_sum(double x) {
 }
 
 // ------------------------------------------------------------------ K1
-// One partial per block.  Blocks walk tiles t = blockIdx.x + k * gridDim.x
-// (gridDim.x == kStatsBlocks, a constant), lanes accumulate their own
-// elements in index order, waves reduce with a fixed xor tree and the four
-// wave sums are added in wave order: the partials, and hence the norm, are
-// bitwise reproducible.
+// Block b of the fixed grid (kStatsBlocks blocks) owns the contiguous flat
+// range [begin + b*chunk, begin + (b+1)*chunk), chunk a multiple of kVec,
+// and walks the segments inside it with a cursor.  Each piece of a segment
+// is a scalar head, a vector body of kVec-element groups (lane j of the
+// block takes groups j, j+256, ...) and a scalar tail.  Lanes accumulate
+// their own elements in index order, waves reduce with a fixed xor tree and
+// the four wave sums are added in wave order, so the per-block partials and
+// hence the norm are bitwise reproducible run to run.
+template <class G, bool kFlat, bool kStats>
+struct GradScan {
+  int umode;
+  float scale, inv;
+  int64_t begin;
+  float* flat;
+  double acc = 0.0;
+  bool bad = false;      // per-element inf/nan tests
+  uint32_t packed = 0;   // packed exponent tests of the vector body
+
+  __device__ void element(const ms_segment_t& sg, int64_t i, bool count) {
+    float g = 0.0f;
+    if (sg.grad) {
+      const typename G::raw r = load_raw1<G>(sg.grad, i - sg.begin);
+      bad |= G::nonfinite(r);
+      g = unscale1(G::widen(r), umode, scale, inv);
+    }
+    if (kStats && count) {
+      const double d = static_cast<double>(g);
+      acc = __builtin_fma(d, d, acc);
+    }
+    if (kFlat) flat[i - begin] = g;
+  }
+
+  __device__ void group(const ms_segment_t& sg, const uint32_t (&w)[kVec * G::kBytes / 4],
+                        int64_t i, bool count) {
+#pragma unroll
+    for (int j = 0; j < kVec * G::kBytes / 4; ++j) packed |= (w[j] & G::kExp) + G::kExpOne;
+    float g[kVec];
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) {
+      g[k] = unscale1(G::widen(word_elem<G>(w, k)), umode, scale, inv);
+      if (kStats && count) {
+        const double d = static_cast<double>(g[k]);
+        acc = __builtin_fma(d, d, acc);
+      }
+    }
+    if (kFlat) store_f8(flat + (i - begin), g);
+  }
+
+  // elements [a, b) of segment sg, all inside or all outside the owned range
+  __device__ void piece(const ms_segment_t& sg, int64_t a, int64_t b, bool count, int lane) {
+    const bool vec = sg.grad != nullptr && aligned16(sg.grad) &&
+                     (!kFlat || aligned16(flat)) && ((sg.begin - begin) & (kVec - 1)) == 0;
+    if (!vec) {
+      if (!sg.grad && !kFlat) return;      // zeros: nothing to count or test
+      for (int64_t i = a + lane; i < b; i += kThreads) element(sg, i, count);
+      return;
+    }
+    const int64_t a8 = sg.begin + (((a - sg.begin) + kVec - 1) & ~int64_t(kVec - 1));
+    const int64_t b8 = sg.begin + ((b - sg.begin) & ~int64_t(kVec - 1));
+    if (a8 >= b8) {
+      for (int64_t i = a + lane; i < b; i += kThreads) element(sg, i, count);
+      return;
+    }
+    for (int64_t i = a + lane; i < a8; i += kThreads) element(sg, i, count);
+    for (int64_t i = b8 + lane; i < b; i += kThreads) element(sg, i, count);
+    const int64_t ng = (b8 - a8) / kVec;
+    const char* src = static_cast<const char*>(sg.grad) + (a8 - sg.begin) * G::kBytes;
+    int64_t j = lane;
+    for (; j + kThreads < ng; j += 2 * kThreads) {   // two groups in flight per lane
+      uint32_t w0[kVec * G::kBytes / 4], w1[kVec * G::kBytes / 4];
+      load_words<G>(src + j * (kVec * G::kBytes), w0);
+      load_words<G>(src + (j + kThreads) * (kVec * G::kBytes), w1);
+      group(sg, w0, a8 + j * kVec, count);
+      group(sg, w1, a8 + (j + kThreads) * kVec, count);
+    }
+    if (j < ng) {
+      uint32_t w0[kVec * G::kBytes / 4];
+      load_words<G>(src + j * (kVec * G::kBytes), w0);
+      group(sg, w0, a8 + j * kVec, count);
+    }
+  }
+};
+
 template <class G, bool kFlat, bool kStats>
 __global__ __launch_bounds__(kThreads) void k_grad_stats(
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
-    int64_t end, int64_t own_begin, int64_t own_end, int unscale,
-    float grad_scale, float* __restrict__ flat, double* __restrict__ bsum,
-    uint32_t* __restrict__ bflag) {
+    int64_t end, int64_t own_begin, int64_t own_end, int umode,
+    float grad_scale, float inv_scale, float* __restrict__ flat,
+    double* __restrict__ bsum, uint32_t* __restrict__ bflag) {
   const int lane = threadIdx.x;
-  double acc = 0.0;
-  bool bad = false;
+  GradScan<G, kFlat, kStats> sc;
+  sc.umode = umode;
+  sc.scale = grad_scale;
+  sc.inv = inv_scale;
+  sc.begin = begin;
+  sc.flat = flat;
   const int64_t n = end - begin;
-  const int64_t ntiles = (n + kTile - 1) / kTile;
-  const bool flat_vec = !kFlat || aligned16(flat);
-
-  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    const int64_t t0 = begin + t * kTile;
-    const int64_t t1 = (t0 + kTile < end) ? t0 + kTile : end;
-    int s = find_seg(segs, nseg, t0);
-    const ms_segment_t seg = segs[s];
-    const bool own_all = t0 >= own_begin && t1 <= own_end;
-    const bool fast = t1 - t0 == kTile && t0 >= seg.begin && t1 <= seg_end(seg) && flat_vec &&
-                      ((t0 - seg.begin) & (kVec - 1)) == 0 &&
-                      aligned16(seg.grad) && own_all;
-    const int64_t i0 = t0 + static_cast<int64_t>(lane) * kVec;
-    if (fast) {
-      float g[kVec];
-      if (seg.grad) {
-        typename G::raw r[kVec];
-        load_raw8<G>(static_cast<const char*>(seg.grad) +
-                         (i0 - seg.begin) * G::kBytes,
-                     r);
-#pragma unroll
-        for (int k = 0; k < kVec; ++k) {
-          bad |= G::nonfinite(r[k]);
-          g[k] = G::widen(r[k]);
-          if (unscale) g[k] = g[k] / grad_scale;
-          if (kStats) {
-            const double d = static_cast<double>(g[k]);
-            acc = __builtin_fma(d, d, acc);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < kVec; ++k) g[k] = 0.0f;
+  int64_t chunk = (n + gridDim.x - 1) / gridDim.x;
+  chunk = (chunk + kVec - 1) & ~int64_t(kVec - 1);
+  const int64_t r0 = begin + static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t r1 = (r0 + chunk < end) ? r0 + chunk : end;
+  if (r0 < r1) {
+    for (int s = find_seg(segs, nseg, r0); s < nseg; ++s) {
+      const ms_segment_t sg = segs[s];
+      const int64_t se = seg_end(sg);
+      const int64_t a = sg.begin > r0 ? sg.begin : r0;
+      const int64_t b = se < r1 ? se : r1;
+      if (a < b) {
+        // split at the owned range so every piece is counted or not
+        const int64_t o0 = own_begin > a ? (own_begin < b ? own_begin : b) : a;
+        const int64_t o1 = own_end < b ? (own_end > o0 ? own_end : o0) : b;
+        if (a < o0) sc.piece(sg, a, o0, false, lane);
+        if (o0 < o1) sc.piece(sg, o0, o1, true, lane);
+        if (o1 < b) sc.piece(sg, o1, b, false, lane);
       }
-      if (kFlat) store_f8(flat + (i0 - begin), g);
-    } else {
-      int sl = s;
-      for (int k = 0; k < kVec; ++k) {
-        const int64_t i = i0 + k;
-        if (i >= t1) break;
-        while (sl + 1 < nseg && i >= seg_end(segs[sl])) ++sl;
-        const ms_segment_t& sg = segs[sl];
-        const bool inside = i >= sg.begin && i < seg_end(sg);
-        float g = 0.0f;
-        if (inside && sg.grad) {
-          const typename G::raw r = load_raw1<G>(sg.grad, i - sg.begin);
-          bad |= G::nonfinite(r);
-          g = G::widen(r);
-          if (unscale) g = g / grad_scale;
-        }
-        if (kStats && i >= own_begin && i < own_end) {
-          const double d = static_cast<double>(g);
-          acc = __builtin_fma(d, d, acc);
-        }
-        if (kFlat) flat[i - begin] = g;
-      }
+      if (se >= r1) break;
     }
   }
-
   if (kStats) {
+    const bool bad = sc.bad || (sc.packed & G::kTop) != 0;
     __shared__ double wsum[kWaves];
     __shared__ uint32_t wbad[kWaves];
-    const double w = wave_sum(acc);
+    const double w = wave_sum(sc.acc);
     const bool wb = __any(bad);
     if ((lane & 63) == 0) {
       wsum[lane >> 6] = w;
@@ -373,8 +458,8 @@ __global__ __launch_bounds__(kThreads) void k_norm_clip(
 // ------------------------------------------------------------------ K3
 struct AdamScalars {
   float neg_lr, decay_alpha, beta1, omb1, beta2, omb2, bc1, bc2, eps,
-      grad_scale;
-  int decay, unscale;
+      grad_scale, inv_scale;
+  int decay, umode;
 };
 
 // One AdamW element, rounding exactly where minispeed's op sequence rounds
@@ -433,8 +518,7 @@ __global__ __launch_bounds__(kThreads) void k_adamw(
                      r);
 #pragma unroll
         for (int k = 0; k < kVec; ++k) {
-          g[k] = G::widen(r[k]);
-          if (h.unscale) g[k] = g[k] / h.grad_scale;
+          g[k] = unscale1(G::widen(r[k]), h.umode, h.grad_scale, h.inv_scale);
         }
       } else {
 #pragma unroll
@@ -469,8 +553,8 @@ __global__ __launch_bounds__(kThreads) void k_adamw(
         if (kFlatGrad) {
           g = flat_grad[l];
         } else if (inside && sg.grad) {
-          g = G::widen(load_raw1<G>(sg.grad, i - sg.begin));
-          if (h.unscale) g = g / h.grad_scale;
+          g = unscale1(G::widen(load_raw1<G>(sg.grad, i - sg.begin)), h.umode,
+                       h.grad_scale, h.inv_scale);
         }
         float p = master[l], m = exp_avg[l], v = exp_avg_sq[l];
         adamw1(g, p, m, v, h, clip, coef);
@@ -540,11 +624,13 @@ int cu_count() {
   return cached;
 }
 
-// Grid of a streaming kernel: enough resident blocks to keep every CU's
-// memory pipeline full, never more blocks than tiles.
+// Grid of a streaming kernel: `blocks_per_cu` resident blocks per CU that
+// walk the tiles grid-stride, or (blocks_per_cu <= 0) one block per tile.
 int stream_grid(int64_t ntiles, int blocks_per_cu) {
-  int64_t g = static_cast<int64_t>(cu_count()) * blocks_per_cu;
+  int64_t g = blocks_per_cu > 0 ? static_cast<int64_t>(cu_count()) * blocks_per_cu
+                                : ntiles;
   if (g > ntiles) g = ntiles;
+  if (g > 0x7fffffff) g = 0x7fffffff;
   if (g < 1) g = 1;
   return static_cast<int>(g);
 }
@@ -552,13 +638,25 @@ int stream_grid(int64_t ntiles, int blocks_per_cu) {
 int env_int(const char* name, int fallback) {
   const char* s = getenv(name);
   if (!s || !*s) return fallback;
-  const int v = atoi(s);
-  return v > 0 ? v : fallback;
+  return atoi(s);
 }
 
 int launch_status() {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MS_OK : static_cast<int>(e);
+}
+
+// How a kernel divides by the loss scale (see unscale1).
+int unscale_mode(int32_t unscale, float scale, float* inv) {
+  *inv = 1.0f;
+  if (!unscale) return 0;
+  int e = 0;
+  const float mant = frexpf(scale, &e);   // scale = mant * 2^e
+  if (mant == 0.5f && e - 1 <= 126 && e - 1 >= -126) {
+    *inv = ldexpf(1.0f, 1 - e);
+    return 1;
+  }
+  return 2;
 }
 
 bool valid_dtype(int32_t d) {
@@ -570,23 +668,24 @@ void launch_stats(const ms_segment_t* segs, int nseg, int64_t begin,
                   int64_t end, int64_t ob, int64_t oe, int unscale, float scale,
                   float* flat, double* bsum, uint32_t* bflag, hipStream_t st) {
   const bool stats = bsum != nullptr;
-  const int64_t ntiles = (end - begin + kTile - 1) / kTile;
+  float inv = 1.0f;
+  const int umode = unscale_mode(unscale, scale, &inv);
   const dim3 block(kThreads);
   if (stats) {
     const dim3 grid(kStatsBlocks);
     if (flat)
       hipLaunchKernelGGL((k_grad_stats<G, true, true>), grid, block, 0, st, segs,
-                         nseg, begin, end, ob, oe, unscale, scale, flat, bsum,
-                         bflag);
+                         nseg, begin, end, ob, oe, umode, scale, inv, flat,
+                         bsum, bflag);
     else
       hipLaunchKernelGGL((k_grad_stats<G, false, true>), grid, block, 0, st,
-                         segs, nseg, begin, end, ob, oe, unscale, scale, flat,
-                         bsum, bflag);
+                         segs, nseg, begin, end, ob, oe, umode, scale, inv,
+                         flat, bsum, bflag);
   } else {
-    const dim3 grid(stream_grid(ntiles, env_int("MS_FLATTEN_BLOCKS_PER_CU", 8)));
+    const dim3 grid(kStatsBlocks);
     hipLaunchKernelGGL((k_grad_stats<G, true, false>), grid, block, 0, st, segs,
-                       nseg, begin, end, ob, oe, unscale, scale, flat, bsum,
-                       bflag);
+                       nseg, begin, end, ob, oe, umode, scale, inv, flat,
+                       bsum, bflag);
   }
 }
 
@@ -596,7 +695,7 @@ void launch_adamw(float* p, float* m, float* v, const float* fg,
                   const AdamScalars& h, const ms_step_scalars_t* sc,
                   hipStream_t st) {
   const int64_t ntiles = (end - begin + kTile - 1) / kTile;
-  const dim3 grid(stream_grid(ntiles, env_int("MS_ADAMW_BLOCKS_PER_CU", 8)));
+  const dim3 grid(stream_grid(ntiles, env_int("MS_ADAMW_BLOCKS_PER_CU", 0)));
   const dim3 block(kThreads);
   if (fg)
     hipLaunchKernelGGL((k_adamw<G, M, true>), grid, block, 0, st, p, m, v, fg,
@@ -721,7 +820,7 @@ int ms_fused_adamw(float* master, float* exp_avg, float* exp_avg_sq,
   h.eps = hp->eps;
   h.grad_scale = hp->grad_scale;
   h.decay = hp->decay != 0;
-  h.unscale = hp->unscale != 0;
+  h.umode = unscale_mode(hp->unscale, hp->grad_scale, &h.inv_scale);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (grad_dtype) {
     case MS_DTYPE_F32:
@@ -749,7 +848,7 @@ int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
   if (!segs || nseg <= 0 || nseg > kMaxSegs) return MS_ETABLE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t ntiles = (end - begin + kTile - 1) / kTile;
-  const dim3 grid(stream_grid(ntiles, env_int("MS_CAST_BLOCKS_PER_CU", 8)));
+  const dim3 grid(stream_grid(ntiles, env_int("MS_CAST_BLOCKS_PER_CU", 0)));
   const dim3 block(kThreads);
   switch (model_dtype) {
     case MS_DTYPE_F32:

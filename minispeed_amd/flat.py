@@ -196,6 +196,9 @@ class SegmentTable:
         return self._dev.data_ptr(), n
 
 
+_ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
+
+
 def _flat_view(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
@@ -253,6 +256,7 @@ class FlatParamGroup:
         # zero_grad skip clearing buffers the fused boundary never wrote.
         self._grad_dirty = False
         self._tables = {}
+        self._rows = None   # static (begin, numel) rows of the whole-range table
 
     # ------------------------------------------------------------- ranges
     @property
@@ -268,16 +272,18 @@ class FlatParamGroup:
     def _pdata_range(self, offset: int, n: int, p: nn.Parameter) -> Range:
         """Flat range covered by ``p.data``: the whole parameter, or the
         owned slice of a ZeRO-3 placeholder (flat.py:103-113)."""
-        if p.data.numel() == n:
+        k = p.numel()
+        if k == n:
             return offset, offset + n
         start = max(offset, self.shard_start)
-        return start, start + p.data.numel()
+        return start, start + k
 
     def model_dtype(self) -> torch.dtype:
-        dtypes = {p.dtype for p in self.params}
-        if len(dtypes) != 1:
-            raise TypeError(f"parameters of one group must share a dtype, got {sorted(map(str, dtypes))}")
-        return next(iter(dtypes))
+        d = self.params[0].dtype
+        if any(p.dtype != d for p in self.params):
+            dtypes = sorted({str(p.dtype) for p in self.params})
+            raise TypeError(f"parameters of one group must share a dtype, got {dtypes}")
+        return d
 
     def table(self, key: str) -> SegmentTable:
         t = self._tables.get(key)
@@ -292,10 +298,11 @@ class FlatParamGroup:
     def model_storages(self) -> List[Optional[tuple]]:
         out = []
         for (offset, p), n in zip(self._offsets, self._numels):
-            d = p.data
-            if not d.is_contiguous():
+            if p.device.type != "cuda":
+                raise RuntimeError(f"parameter on {p.device}; the flat group lives on a HIP device")
+            if not p.is_contiguous():
                 raise RuntimeError("parameter data must be contiguous")
-            out.append(self._storage(d, self._pdata_range(offset, n, p)))
+            out.append((p.data_ptr(), self._pdata_range(offset, n, p), p.element_size()))
         return out
 
     # -------------------------------------------------------- conversions
@@ -364,6 +371,90 @@ class FlatParamGroup:
         for (offset, p), n in zip(self._offsets, self._numels):
             lo, hi = _overlap((offset, offset + n), (self.shard_start, self.shard_end))
             p.data = torch.empty(max(0, hi - lo), dtype=p.data.dtype, device=p.data.device)
+
+    # ------------------------------------------------ boundary pointers
+    @property
+    def whole_range(self) -> bool:
+        """The owned range is the whole padded space (world size 1)."""
+        return self.shard_start == 0 and self.shard_end == self.numel_padded
+
+    def _check_grad(self, g: torch.Tensor, n: int, dtype: torch.dtype) -> torch.Tensor:
+        if g.numel() != n:
+            raise RuntimeError(f"gradient of a parameter has {g.numel()} elements, expected {n}")
+        if g.dtype != dtype:
+            raise TypeError(f"gradient dtype {g.dtype} differs from parameter dtype {dtype}")
+        if g.device != self.device:
+            raise RuntimeError(f"gradient on {g.device}, expected {self.device}")
+        return g.contiguous()
+
+    def grad_pointers(self) -> Tuple[List[int], List[torch.Tensor]]:
+        """Device address of every parameter's gradient (0: no gradient) and
+        the tensors behind them, which the caller keeps alive until the
+        kernels reading them have run."""
+        dtype = self.model_dtype()
+        dev = self.device
+        ptrs: List[int] = []
+        keep: List[torch.Tensor] = []
+        for p, n in zip(self.params, self._numels):
+            g = p.grad
+            if g is None:
+                ptrs.append(0)
+                continue
+            if g.dtype != dtype or g.numel() != n or g.device != dev or not g.is_contiguous():
+                g = self._check_grad(g, n, dtype)
+            ptrs.append(g.data_ptr())
+            keep.append(g)
+        return ptrs, keep
+
+    def model_pointers(self) -> List[int]:
+        """Device address of every parameter's storage (the cast target)."""
+        ptrs = []
+        for p in self.params:
+            if not p.is_contiguous():
+                raise RuntimeError("parameter data must be contiguous")
+            ptrs.append(p.data_ptr())
+        return ptrs
+
+    def boundary_table(self, lo: int, hi: int, gptrs: Optional[List[int]],
+                       mptrs: Optional[List[int]]) -> np.ndarray:
+        """Segment table of ``[lo, hi)`` with the given grad / model
+        addresses (``None``: no such storage).  For the whole padded range
+        with full-size parameters the rows are static and only the two
+        pointer columns are filled in."""
+        n_params = len(self.params)
+        full = all(p.numel() == n for p, n in zip(self.params, self._numels)) if mptrs else True
+        if lo == 0 and hi == self.numel_padded and full:
+            if self._rows is None:
+                rows, idx = [], []
+                for i, (off, n) in enumerate(zip(self.layout.offsets, self._numels)):
+                    if n:
+                        rows.append((off, n))
+                        idx.append(i)
+                if self.numel_padded > self.numel:
+                    rows.append((self.numel, self.numel_padded - self.numel))
+                    idx.append(n_params)
+                base = np.zeros((len(rows), 4), dtype=np.int64)
+                base[:, :2] = np.asarray(rows, dtype=np.int64).reshape(-1, 2)
+                check_table(base, 0, self.numel_padded)
+                self._rows = (base, np.asarray(idx, dtype=np.int64))
+            base, idx = self._rows
+            table = base.copy()
+            if gptrs is not None:
+                table[:, 2] = np.asarray(list(gptrs) + [0], dtype=np.uint64).astype(np.int64)[idx]
+            if mptrs is not None:
+                table[:, 3] = np.asarray(list(mptrs) + [0], dtype=np.uint64).astype(np.int64)[idx]
+            return table
+        esz_g = _ELEM_BYTES[self.model_dtype()]
+        grads = [None] * n_params
+        models = [None] * n_params
+        for i, ((off, p), n) in enumerate(zip(self._offsets, self._numels)):
+            if gptrs is not None and gptrs[i]:
+                grads[i] = (gptrs[i], (off, off + n), esz_g)
+            if mptrs is not None and mptrs[i]:
+                models[i] = (mptrs[i], self._pdata_range(off, n, p), p.element_size())
+        table = self.layout.segments(lo, hi, grads, models)
+        check_table(table, lo, hi)
+        return table
 
     # ----------------------------------------------------------- grads
     def grad_storages(self) -> Tuple[List[Optional[tuple]], List[torch.Tensor]]:

@@ -17,7 +17,7 @@ from typing import List, Optional
 import torch
 
 from .. import comm
-from ..boundary import GroupLaunch, Workspace, run_boundary
+from ..boundary import GroupLaunch, LaunchTimer, Workspace, run_boundary
 from ..flat import FlatParamGroup
 from ..optim.adam import FlatAdam
 
@@ -33,6 +33,7 @@ class ZeROOptimizer:
         self.adam = FlatAdam(flat_groups, option_groups, zero_stage=zero_stage)
         self.grad_norm: Optional[float] = None
         self._workspace: Optional[Workspace] = None
+        self.launch_timer: Optional[LaunchTimer] = None  # HIP-event timing hook
 
     # ------------------------------------------------------ torch-ish surface
     @property
@@ -78,9 +79,10 @@ class ZeROOptimizer:
             self._workspace = Workspace(self.flat_groups[0].device, len(self.flat_groups))
         return self._workspace
 
-    def _model_targets(self) -> List[Optional[List[Optional[tuple]]]]:
-        """Where K3 writes the model-dtype copy of each group."""
-        return [g.model_storages() for g in self.flat_groups]
+    def _model_targets(self) -> List[Optional[List[int]]]:
+        """Where K3 writes the model-dtype copy of each group (addresses of
+        the parameters' storage)."""
+        return [g.model_pointers() for g in self.flat_groups]
 
     def _after_boundary(self, overflow: bool) -> None:
         """Stage-specific follow-up once the scalars are on the host."""
@@ -98,24 +100,24 @@ class ZeROOptimizer:
         keep: List[torch.Tensor] = []
         grads = []
         for g in self.flat_groups:
-            stores, tensors = g.grad_storages()
-            grads.append(stores)
+            ptrs, tensors = g.grad_pointers()
+            grads.append(ptrs)
             keep.extend(tensors)
             g.release_grads()
         models = self._model_targets()
         launches = []
-        for g, group, state, gstores, mstores in zip(
+        for g, group, state, gptrs, mptrs in zip(
             self.flat_groups, self.adam.param_groups, self.adam.state, grads, models
         ):
             lr, betas, eps, wd = FlatAdam.hyper(group)
             launches.append(GroupLaunch(
                 group=g, lr=lr, betas=betas, eps=eps, weight_decay=wd,
                 step=state["step"] + 1, exp_avg=state["exp_avg"], exp_avg_sq=state["exp_avg_sq"],
-                grads=gstores, model=mstores,
+                grads=gptrs, model=mptrs,
             ))
         scalars = run_boundary(
             launches, ws, scaler=scaler, max_norm=max_norm,
-            materialize_flat_grad=materialize_flat_grad,
+            materialize_flat_grad=materialize_flat_grad, timer=self.launch_timer,
         )
         del keep  # the read-back synchronised the stream
         overflow = bool(scalars.overflow)

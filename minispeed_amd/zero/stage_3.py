@@ -70,7 +70,7 @@ class ZeROStage3Optimizer(ZeROOptimizer):
         return True
 
     # ------------------------------------------------------ fused boundary
-    def _model_targets(self) -> List[Optional[List[Optional[tuple]]]]:
+    def _model_targets(self) -> List[Optional[List[int]]]:
         if not self._gathered:
             # the reference's free_parameters is a no-op then: nothing written
             self._boundary_freed = False
@@ -78,7 +78,7 @@ class ZeROStage3Optimizer(ZeROOptimizer):
         for g in self.flat_groups:
             g.dematerialize_params()
         self._boundary_freed = True
-        return [g.model_storages() for g in self.flat_groups]
+        return [g.model_pointers() for g in self.flat_groups]
 
     def _after_boundary(self, overflow: bool) -> None:
         if self._boundary_freed:

@@ -407,6 +407,25 @@ class Engine:
         self.global_steps += 1
         return True
 
+    def load_state(self, masters, exp_avgs, exp_avg_sqs, steps, scaler_state, lr_epoch,
+                   lrs) -> None:
+        """Start from a given state (fp32 tensors per group, Adam step
+        counters, (scale, good_steps, skipped_steps), scheduler epoch, current
+        lrs); the model parameters are refreshed from the masters."""
+        for g, d, m, v, st, k, lr in zip(self.groups, masters, exp_avgs, exp_avg_sqs, self.state,
+                                         steps, lrs):
+            g.data.copy_(d)
+            st["exp_avg"].copy_(m)
+            st["exp_avg_sq"].copy_(v)
+            st["step"] = int(k)
+        for pg, lr in zip(self.param_groups, lrs):
+            pg["lr"] = lr
+        self.scaler.scale, self.scaler.good_steps, self.scaler.skipped_steps = scaler_state
+        self.scheduler.last_epoch = lr_epoch
+        for g in self.groups:
+            if not g.partitioned:
+                g.copy_flat_to_model()
+
     def step(self) -> bool:                                               # engine.py:254-266
         if not (self.micro_steps > 0 and self.micro_steps % self.gas == 0):
             return False

@@ -1,0 +1,321 @@
+"""Engine behaviour on the GPU, the properties minispeed's own test suite
+asserts (tests/test_engine.py, tests/test_gpu.py, tests/test_zero3.py),
+with the boundary step running as the HIP kernels."""
+
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+import minispeed_amd as ms
+from minispeed_amd.flat import FlatParamGroup
+from minispeed_amd.precision import has_overflow
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+STEPS, GAS, MICRO = 6, 2, 4
+
+
+class MLP(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.net = nn.Sequential(nn.Linear(8, 32), nn.Tanh(), nn.Linear(32, 32), nn.ReLU(),
+                                 nn.LayerNorm(32), nn.Linear(32, 1))
+
+    def forward(self, x):
+        return self.net(x)
+
+
+def build_model(seed=1234):
+    torch.manual_seed(seed)
+    return MLP().to(DEV)
+
+
+def make_batch(steps, gas, micro, seed=7):
+    g = torch.Generator().manual_seed(seed)
+    n = steps * gas * micro
+    x = torch.randn(n, 8, generator=g).view(steps, gas, micro, 8)
+    y = torch.randn(n, 1, generator=g).view(steps, gas, micro, 1)
+    return x.to(DEV), y.to(DEV)
+
+
+def config(micro=MICRO, gas=GAS, lr=1e-3, wd=0.01, clip=1.0, dtype="fp32", stage=0,
+           warmup=0, total=None, scheduler="WarmupLR", power=8, window=100, materialize=False):
+    sp = {"warmup_min_lr": 0.0, "warmup_max_lr": lr, "warmup_num_steps": warmup}
+    if total is not None:
+        sp["total_num_steps"] = total
+    cfg = {"train_micro_batch_size_per_gpu": micro, "gradient_accumulation_steps": gas,
+           "gradient_clipping": clip, "dtype": dtype,
+           "optimizer": {"type": "AdamW", "params": {"lr": lr, "betas": [0.9, 0.999], "eps": 1e-8,
+                                                      "weight_decay": wd}},
+           "scheduler": {"type": scheduler, "params": sp},
+           "zero_optimization": {"stage": stage}, "steps_per_print": 1000,
+           "hip_boundary": {"materialize_flat_grad": materialize}}
+    if dtype == "fp16":
+        cfg["fp16"] = {"enabled": True, "loss_scale": 0, "initial_scale_power": power,
+                       "loss_scale_window": window}
+    elif dtype == "bf16":
+        cfg["bf16"] = {"enabled": True}
+    return cfg
+
+
+def mse(pred, y):
+    return F.mse_loss(pred.float(), y.float())
+
+
+def train(engine, x, y, steps, gas):
+    losses = []
+    engine.train()
+    for s in range(steps):
+        for m in range(gas):
+            loss = mse(engine(x[s, m]), y[s, m])
+            losses.append(float(loss.detach()))
+            engine.backward(loss)
+            engine.step()
+    return losses
+
+
+def test_engine_matches_textbook_adamw_with_clipping():
+    """minispeed tests/test_engine.py:45-64: engine == torch.optim.AdamW +
+    clip_grad_norm_ at rtol 1e-4."""
+    lr, wd, clip = 1e-3, 0.01, 1.0
+    x, y = make_batch(STEPS, GAS, MICRO)
+    ref = build_model()
+    opt = torch.optim.AdamW(ref.parameters(), lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+    ref_losses = []
+    for s in range(STEPS):
+        for m in range(GAS):
+            loss = F.mse_loss(ref(x[s, m]), y[s, m]) / GAS
+            ref_losses.append(float(loss.detach()) * GAS)
+            loss.backward()
+        torch.nn.utils.clip_grad_norm_(ref.parameters(), clip)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+    model = build_model()
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=config(lr=lr, wd=wd, clip=clip))
+    losses = train(engine, x, y, STEPS, GAS)
+    assert engine.global_steps == STEPS
+    np.testing.assert_allclose(losses, ref_losses, rtol=1e-4, atol=1e-6)
+    for a, b in zip(model.parameters(), ref.parameters()):
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-6)
+
+
+def test_gradient_accumulation_equals_large_batch():
+    x, y = make_batch(STEPS, GAS, MICRO)
+    big = build_model()
+    e_big = ms.initialize(model=big, model_parameters=list(big.parameters()),
+                          config=config(micro=MICRO * GAS, gas=1, lr=5e-3, wd=0.0, clip=None))
+    train(e_big, x.reshape(STEPS, 1, GAS * MICRO, 8), y.reshape(STEPS, 1, GAS * MICRO, 1), STEPS, 1)
+    acc = build_model()
+    e_acc = ms.initialize(model=acc, model_parameters=list(acc.parameters()),
+                          config=config(lr=5e-3, wd=0.0, clip=None))
+    train(e_acc, x, y, STEPS, GAS)
+    for a, b in zip(acc.parameters(), big.parameters()):
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-6)
+
+
+def test_step_applies_once_per_boundary_and_tuple_unpacking():
+    model = build_model()
+    engine, optimizer, none, sched = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                                                   config=config())
+    assert optimizer is engine.optimizer and sched is engine.lr_scheduler and none is None
+    x, y = make_batch(1, GAS, MICRO)
+    applied = []
+    for m in range(GAS):
+        engine.backward(mse(engine(x[0, m]), y[0, m]))
+        applied.append(engine.step())
+        assert engine.is_gradient_accumulation_boundary == (m == GAS - 1)
+    assert applied == [False, True]
+    assert engine.step() is False and engine.global_steps == 1
+    assert all(p.grad is None for p in model.parameters())     # released at the boundary
+
+
+def test_bf16_learns_with_fp32_masters():
+    x, y = make_batch(STEPS, GAS, MICRO)
+    model = build_model()
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=config(dtype="bf16", lr=1e-2, clip=None))
+    losses = train(engine, x, y, STEPS, GAS)
+    assert np.all(np.isfinite(losses)) and losses[-1] < losses[0]
+    assert next(model.parameters()).dtype == torch.bfloat16
+    assert engine.flat_groups[0].data.dtype == torch.float32
+    assert engine.get_loss_scale() == 1.0
+    for (off, p), n in zip(engine.flat_groups[0]._offsets, engine.flat_groups[0]._numels):
+        want = engine.flat_groups[0].data[off:off + n].to(torch.bfloat16).view(p.shape)
+        assert torch.equal(p.data.view(torch.int16), want.view(torch.int16))
+
+
+def test_fp16_trains_and_scale_grows():
+    x, y = make_batch(STEPS, GAS, MICRO)
+    model = build_model()
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=config(dtype="fp16", power=4, window=3, lr=1e-2, clip=1.0))
+    losses = train(engine, x, y, STEPS, GAS)
+    assert np.all(np.isfinite(losses)) and losses[-1] < losses[0]
+    assert next(model.parameters()).dtype == torch.float16
+    assert engine.get_loss_scale() > 2.0 ** 4 and engine.loss_scaler.skipped_steps == 0
+    assert engine.grad_norm is not None and engine.grad_norm > 0
+
+
+@pytest.mark.parametrize("stage", [0, 2, 3])
+def test_fp16_forced_inf_skips_step(stage):
+    """minispeed tests/test_gpu.py:51-89 and tests/test_zero3.py:184-210."""
+    x, y = make_batch(STEPS + 2, GAS, MICRO)
+    model = build_model()
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=config(dtype="fp16", power=6, lr=1e-2, clip=1.0, warmup=5,
+                                         stage=stage))
+    train(engine, x, y, 1, GAS)
+    for m in range(GAS):
+        engine.backward(mse(engine(x[1, m]), y[1, m]))
+    for p in model.parameters():
+        if p.grad is not None and p.grad.numel():
+            p.grad.reshape(-1)[0] = float("inf")
+            break
+    steps0, scale0, lr0 = engine.global_steps, engine.get_loss_scale(), engine.lr_scheduler.get_last_lr()
+    masters0 = engine.flat_groups[0].data.clone()
+    moments0 = [st["exp_avg"].clone() for st in engine.optimizer.state]
+    before = {n: p.detach().clone() for n, p in model.named_parameters()}
+    assert engine.step() is False
+    assert engine.global_steps == steps0 and engine.skipped_steps == 1
+    assert engine.get_loss_scale() == scale0 / 2
+    assert engine.lr_scheduler.get_last_lr() == lr0
+    assert torch.equal(engine.flat_groups[0].data, masters0)
+    assert all(torch.equal(a["exp_avg"], b) for a, b in zip(engine.optimizer.state, moments0))
+    assert [st["step"] for st in engine.optimizer.state] == [steps0]
+    if stage < 3:
+        for n, p in model.named_parameters():
+            assert torch.equal(p.view(torch.int16), before[n].view(torch.int16))
+    else:
+        assert not engine.optimizer.params_gathered
+        assert engine.flat_groups[0].grad is None
+    losses = train(engine, x[2:], y[2:], 2, GAS)
+    assert np.all(np.isfinite(losses)) and engine.global_steps == steps0 + 2
+
+
+def test_stage3_matches_stage0():
+    x, y = make_batch(4, GAS, MICRO)
+    out = {}
+    for stage in (0, 3):
+        model = build_model()
+        engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                               config=config(stage=stage))
+        losses = train(engine, x, y, 4, GAS)
+        out[stage] = (losses, {k: v.clone() for k, v in engine.state_dict().items()}, engine)
+    np.testing.assert_allclose(out[3][0], out[0][0], rtol=1e-5, atol=1e-7)
+    for k, v in out[0][1].items():
+        torch.testing.assert_close(out[3][1][k], v, rtol=1e-5, atol=1e-7)
+    assert out[3][2].global_steps == out[0][2].global_steps == 4
+
+
+def test_stage3_lifecycle():
+    """minispeed tests/test_zero3.py:51-91."""
+    x, y = make_batch(1, GAS, MICRO)
+    model = build_model()
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=config(stage=3))
+    g = engine.flat_groups[0]
+    shapes = [p.shape for p in build_model().parameters()]
+    assert not engine.optimizer.params_gathered
+    assert all(p.data.dim() == 1 for p in model.parameters()) and g.grad is None
+    loss = mse(engine(x[0, 0]), y[0, 0])
+    assert engine.optimizer.params_gathered
+    assert [p.shape for p in model.parameters()] == shapes
+    engine.backward(loss)
+    assert engine.step() is False and engine.optimizer.params_gathered
+    engine.backward(mse(engine(x[0, 1]), y[0, 1]))
+    assert engine.step() is True
+    assert not engine.optimizer.params_gathered
+    assert all(p.data.dim() == 1 for p in model.parameters())
+    assert g.grad is None and g.data.numel() == g.numel_shard()
+    assert engine.optimizer.state[0]["exp_avg"].numel() == g.numel_shard()
+    raw = model.state_dict()
+    full = engine.state_dict()
+    for k in full:
+        assert raw[k].dim() == 1 and full[k].shape.numel() == raw[k].numel()
+    engine.eval()
+    with torch.no_grad():
+        assert engine(x[0, 0]).shape == (MICRO, 1)
+
+
+def test_stage3_partition_roundtrip_as_one_rank_of_two():
+    """minispeed tests/test_zero3.py:94-147, on device buffers."""
+    torch.manual_seed(0)
+    params = [nn.Parameter(torch.randn(7, 5, device=DEV)), nn.Parameter(torch.randn(3, device=DEV))]
+    originals = [p.data.clone() for p in params]
+    g = FlatParamGroup(params, rank=1, world_size=2, zero_stage=3, device=torch.device(DEV))
+    g.copy_model_to_flat()
+    g.partition_params()
+    assert g.data.numel() == g.numel_padded // 2 and g.shard_start == g.numel_padded // 2
+    assert sum(p.numel() for p in params) == g.numel_shard()
+    assert all(p.data.dim() == 1 for p in params)
+    full = torch.cat([o.reshape(-1) for o in originals] + [torch.zeros(g.numel_padded - g.numel, device=DEV)])
+    g.materialize_params()
+    g.copy_flat_to_model(full)
+    for p, o in zip(params, originals):
+        assert torch.equal(p.data, o)
+    g.dematerialize_params()
+    g.copy_flat_to_model()
+    off = 0
+    for p, o in zip(params, originals):
+        n = o.numel()
+        lo, hi = max(off, g.shard_start), min(off + n, g.shard_end)
+        assert p.data.numel() == max(0, hi - lo)
+        if hi > lo:
+            assert torch.equal(p.data, o.reshape(-1)[lo - off:hi - off])
+        off += n
+    g.materialize_params()
+    g.copy_flat_to_model(full)
+    for p, o in zip(params, originals):
+        assert torch.equal(p.data, o)
+
+
+@pytest.mark.parametrize("dtype,stage", [("fp16", 2), ("bf16", 1), ("fp32", 3), ("fp16", 3)])
+def test_materialized_flat_grad_mode_is_bitwise_identical(dtype, stage):
+    x, y = make_batch(3, GAS, MICRO)
+    res = []
+    for materialize in (False, True):
+        model = build_model()
+        engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                               config=config(dtype=dtype, stage=stage, materialize=materialize,
+                                             lr=1e-2))
+        train(engine, x, y, 3, GAS)
+        res.append((engine.flat_groups[0].data.clone(),
+                     engine.optimizer.state[0]["exp_avg_sq"].clone(), engine.grad_norm))
+        g = engine.flat_groups[0]
+        if stage < 3:
+            assert not g.grad.any()          # zero after the boundary, as in the reference
+        else:
+            assert g.grad is None
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    assert res[0][2] == res[1][2]
+
+
+def test_has_overflow_on_device_buffers():
+    assert not has_overflow(torch.zeros(4, device=DEV))
+    assert has_overflow(torch.tensor([1.0, float("inf")], device=DEV))
+    assert has_overflow(torch.tensor([float("nan")], device=DEV, dtype=torch.float16))
+    assert has_overflow(torch.zeros(2, device=DEV), torch.tensor([float("-inf")], device=DEV,
+                                                                 dtype=torch.bfloat16))
+    big = torch.zeros(3_000_001, device=DEV)
+    big[2_999_999] = float("nan")
+    assert has_overflow(big) and not has_overflow(big[:2_999_999])
+
+
+def test_two_param_groups_with_own_hyperparameters():
+    model = build_model()
+    groups = [{"params": list(model.net[0].parameters()), "lr": 3e-3, "weight_decay": 0.0},
+              {"params": [p for m in list(model.net)[1:] for p in m.parameters()]}]
+    engine = ms.initialize(model=model, model_parameters=groups, config=config(lr=1e-3))
+    assert len(engine.flat_groups) == 2
+    assert [g["lr"] for g in engine.optimizer.param_groups] == [3e-3, 1e-3]
+    x, y = make_batch(2, GAS, MICRO)
+    train(engine, x, y, 2, GAS)
+    assert engine.global_steps == 2
+    assert all(st["step"] == 2 for st in engine.optimizer.state)

@@ -1,0 +1,116 @@
+"""The C-ABI library on the CPU: it loads, exports exactly what
+include/minispeed_boundary.h declares, its structs have the header's layout,
+and host-side argument errors come back as codes before anything launches.
+No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from minispeed_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "minispeed_boundary.h")
+
+
+def _declared_functions():
+    text = open(HEADER, encoding="utf-8").read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ms_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_with_matching_abi():
+    lib = _native.load()
+    assert lib.ms_abi_version() == _native.ABI_VERSION
+    assert _native.stats_blocks() >= 256
+
+
+def test_every_declared_symbol_is_exported_and_typed():
+    declared = _declared_functions()
+    assert "ms_fused_adamw" in declared and len(declared) >= 7
+    lib = ctypes.CDLL(_native.library_path())
+    for name in declared:
+        assert hasattr(lib, name), name
+        assert name in _native.SIGNATURES, name
+    assert set(_native.SIGNATURES) == set(declared)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layout_matches_header(tmp_path):
+    src = tmp_path / "probe.c"
+    src.write_text(r'''
+#include <stddef.h>
+#include <stdio.h>
+#include "minispeed_boundary.h"
+#define F(T, m) printf(#T "." #m " %zu\n", offsetof(T, m));
+int main(void) {
+  printf("ms_segment_t %zu\n", sizeof(ms_segment_t));
+  F(ms_segment_t, begin) F(ms_segment_t, numel) F(ms_segment_t, grad) F(ms_segment_t, model)
+  printf("ms_step_scalars_t %zu\n", sizeof(ms_step_scalars_t));
+  F(ms_step_scalars_t, overflow) F(ms_step_scalars_t, clip_applied) F(ms_step_scalars_t, sumsq)
+  F(ms_step_scalars_t, norm) F(ms_step_scalars_t, coef) F(ms_step_scalars_t, coef64)
+  F(ms_step_scalars_t, next_scale) F(ms_step_scalars_t, next_good_steps)
+  F(ms_step_scalars_t, next_skipped_steps)
+  printf("ms_adamw_params_t %zu\n", sizeof(ms_adamw_params_t));
+  F(ms_adamw_params_t, neg_lr) F(ms_adamw_params_t, bias_c2) F(ms_adamw_params_t, grad_scale)
+  F(ms_adamw_params_t, decay) F(ms_adamw_params_t, unscale)
+  return 0;
+}
+''')
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = dict(line.rsplit(" ", 1) for line in lines if line)
+    classes = {"ms_segment_t": _native.Segment, "ms_step_scalars_t": _native.StepScalars,
+               "ms_adamw_params_t": _native.AdamWParams}
+    for key, value in got.items():
+        if "." in key:
+            cname, field = key.split(".")
+            assert getattr(classes[cname], field).offset == int(value), key
+        else:
+            assert ctypes.sizeof(classes[key]) == int(value), key
+
+
+def test_host_argument_errors_return_codes_without_launching():
+    lib = _native.load()
+    EINVAL, ETABLE, EBLOCKS = -1, -2, -3
+    nb = _native.stats_blocks()
+    # bad dtype / negative range / missing outputs / small workspace / empty table
+    assert lib.ms_grad_stats(None, 0, 7, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb, None) == EINVAL
+    assert lib.ms_grad_stats(None, 0, 1, 10, 5, 0, 10, 0, 1.0, None, 8, 8, nb, None) == EINVAL
+    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, None, None, nb, None) == EINVAL
+    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb - 1, None) == EBLOCKS
+    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb, None) == ETABLE
+    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 1, 0.0, 8, None, None, nb, None) == ETABLE
+    assert lib.ms_norm_clip(None, None, nb, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, None, None) == EINVAL
+    assert lib.ms_norm_clip(8, 8, nb - 1, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None) == EBLOCKS
+    assert lib.ms_norm_clip(8, 8, nb, 1, 0, 0.0, 0, 1.0, 0, 0, 0, 1.0, 1.0, 8, None) == EINVAL
+    hp = _native.AdamWParams()
+    assert lib.ms_fused_adamw(8, 8, 8, None, None, 0, 9, 1, 0, 10, ctypes.byref(hp), 8, None) == EINVAL
+    assert lib.ms_fused_adamw(8, 8, 8, None, None, 0, 1, 1, 0, 10, None, 8, None) == EINVAL
+    assert lib.ms_fused_adamw(8, 8, 8, None, None, 0, 1, 1, 0, 10, ctypes.byref(hp), 8, None) == ETABLE
+    assert lib.ms_fused_adamw(None, None, None, None, None, 0, 1, 1, 4, 4, ctypes.byref(hp), 8, None) == 0
+    hp.unscale = 1
+    hp.grad_scale = 0.0
+    assert lib.ms_fused_adamw(8, 8, 8, None, 8, 1, 1, 1, 0, 10, ctypes.byref(hp), 8, None) == EINVAL
+    assert lib.ms_cast_to_model(None, 0, 10, 8, 1, 1, None) == EINVAL
+    assert lib.ms_cast_to_model(8, 0, 10, None, 0, 1, None) == ETABLE
+    assert lib.ms_cast_to_model(8, 0, 10, 8, 1, 5, None) == EINVAL
+    assert lib.ms_cast_to_model(None, 3, 3, None, 0, 1, None) == 0
+    for code in (0, EINVAL, ETABLE, EBLOCKS):
+        assert lib.ms_error_string(code)
+    with pytest.raises(RuntimeError, match="segment count"):
+        _native.check(ETABLE, "probe")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setenv("MINISPEED_AMD_LIB", str(tmp_path / "absent.so"))
+    monkeypatch.setattr(_native, "_lib", None)
+    with pytest.raises(_native.NativeLibraryError):
+        _native.load()
