@@ -23,7 +23,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import List, Optional, Sequence
+from typing import Callable, List, Optional, Sequence
 
 import numpy as np
 import torch
@@ -143,23 +143,6 @@ class GroupLaunch:
     exp_avg: torch.Tensor         # owned-range moments (optim/adam.py:58-65)
     exp_avg_sq: torch.Tensor
     grads: List[int]              # gradient address per parameter (0: none)
-    model: Optional[List[int]]    # cast target per parameter, None: no write
-
-
-def _tables(gl: GroupLaunch):
-    """(K1 table over [0, N), K3 table over the owned range), uploaded.
-
-    At world size 1 both ranges are the whole padded space and one table
-    (gradient and model addresses) serves both kernels."""
-    g = gl.group
-    lo, hi = g.own_range
-    if g.whole_range:
-        t = g.boundary_table(0, g.numel_padded, gl.grads, gl.model)
-        dev = g.table("boundary").upload(t)
-        return dev, dev
-    t1 = g.boundary_table(0, g.numel_padded, gl.grads, None)
-    t3 = g.boundary_table(lo, hi, gl.grads, gl.model)
-    return g.table("k1").upload(t1), g.table("k3").upload(t3)
 
 
 def run_boundary(
@@ -169,12 +152,16 @@ def run_boundary(
     scaler,
     max_norm: Optional[float],
     materialize_flat_grad: bool,
+    model_targets: Callable[[], List[Optional[List[int]]]],
     timer: Optional[LaunchTimer] = None,
 ) -> _native.StepScalars:
     """Launch the whole boundary and return K2's scalars (one host sync).
 
-    The caller keeps the gradient tensors behind ``GroupLaunch.grads``
-    referenced until this returns.
+    K1 and K2 are launched as soon as the gradient addresses are known;
+    ``model_targets()`` (the addresses K3 casts the updated masters into, per
+    group; ``None`` for no write) is called after that, so whatever it does
+    on the host overlaps K1 on the device.  The caller keeps the gradient
+    tensors behind ``GroupLaunch.grads`` referenced until this returns.
     """
     lib = _native.load()
     device = ws.device
@@ -184,7 +171,7 @@ def run_boundary(
     scale32 = _f32(scale)
     timer = timer or _NO_TIMER
 
-    prepared = []
+    dtypes, flats = [], []
     for gi, gl in enumerate(launches):
         g = gl.group
         dtype = _native.ms_dtype(g.model_dtype())
@@ -195,20 +182,7 @@ def run_boundary(
             flat_out = g.grad
             g._grad_dirty = True
         lo, hi = g.own_range
-        master = g.shard
-        if master.numel() != hi - lo or gl.exp_avg.numel() != hi - lo or gl.exp_avg_sq.numel() != hi - lo:
-            raise RuntimeError(
-                f"grad/shard shape mismatch: owned range {hi - lo} vs master {master.numel()}, "
-                f"moments {gl.exp_avg.numel()}/{gl.exp_avg_sq.numel()}"
-            )
-        t1, t3 = _tables(gl)
-        hp = adamw_params(gl.lr, gl.betas, gl.eps, gl.weight_decay, gl.step,
-                          grad_scale=scale, unscale=unscale and flat_out is None)
-        prepared.append((gi, gl, dtype, flat_out, t1, t3, hp, master))
-
-    for gi, gl, dtype, flat_out, t1, t3, hp, master in prepared:
-        g = gl.group
-        lo, hi = g.own_range
+        t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None))
         psum, pflag = ws.partial_ptrs(gi)
         tok = timer.start("k1")
         rc = lib.ms_grad_stats(
@@ -218,6 +192,8 @@ def run_boundary(
         )
         timer.stop(tok)
         _native.check(rc, "ms_grad_stats")
+        dtypes.append(dtype)
+        flats.append(flat_out)
 
     tok = timer.start("k2")
     rc = lib.ms_norm_clip(
@@ -231,11 +207,21 @@ def run_boundary(
     timer.stop(tok)
     _native.check(rc, "ms_norm_clip")
 
-    for gi, gl, dtype, flat_out, t1, t3, hp, master in prepared:
+    models = model_targets()
+    for gl, dtype, flat_out, mptrs in zip(launches, dtypes, flats, models):
         g = gl.group
         lo, hi = g.own_range
         if hi <= lo:
             continue
+        master = g.shard
+        if master.numel() != hi - lo or gl.exp_avg.numel() != hi - lo or gl.exp_avg_sq.numel() != hi - lo:
+            raise RuntimeError(
+                f"grad/shard shape mismatch: owned range {hi - lo} vs master {master.numel()}, "
+                f"moments {gl.exp_avg.numel()}/{gl.exp_avg_sq.numel()}"
+            )
+        t3 = g.table("k3").upload(g.boundary_table(lo, hi, gl.grads, mptrs))
+        hp = adamw_params(gl.lr, gl.betas, gl.eps, gl.weight_decay, gl.step,
+                          grad_scale=scale, unscale=unscale and flat_out is None)
         fg_ptr = flat_out.data_ptr() + lo * 4 if flat_out is not None else None
         tok = timer.start("k3")
         rc = lib.ms_fused_adamw(

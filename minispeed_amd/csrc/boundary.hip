@@ -39,7 +39,8 @@ constexpr int kThreads = 256;             // 4 wave64 per block
 constexpr int kWaves = kThreads / 64;
 constexpr int kVec = 8;                   // elements per lane per tile
 constexpr int kTile = kThreads * kVec;    // 2048 flat elements
-constexpr int kStatsBlocks = 2048;        // fixed K1 grid (determinism)
+constexpr int kStatsBlocks = 4096;        // fixed K1 grid (determinism)
+constexpr int kScanThreads = 512;         // K1 block: 8 wave64
 constexpr int kMaxSegs = 1 << 26;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -284,26 +285,26 @@ struct GradScan {
                      (!kFlat || aligned16(flat)) && ((sg.begin - begin) & (kVec - 1)) == 0;
     if (!vec) {
       if (!sg.grad && !kFlat) return;      // zeros: nothing to count or test
-      for (int64_t i = a + lane; i < b; i += kThreads) element(sg, i, count);
+      for (int64_t i = a + lane; i < b; i += kScanThreads) element(sg, i, count);
       return;
     }
     const int64_t a8 = sg.begin + (((a - sg.begin) + kVec - 1) & ~int64_t(kVec - 1));
     const int64_t b8 = sg.begin + ((b - sg.begin) & ~int64_t(kVec - 1));
     if (a8 >= b8) {
-      for (int64_t i = a + lane; i < b; i += kThreads) element(sg, i, count);
+      for (int64_t i = a + lane; i < b; i += kScanThreads) element(sg, i, count);
       return;
     }
-    for (int64_t i = a + lane; i < a8; i += kThreads) element(sg, i, count);
-    for (int64_t i = b8 + lane; i < b; i += kThreads) element(sg, i, count);
+    for (int64_t i = a + lane; i < a8; i += kScanThreads) element(sg, i, count);
+    for (int64_t i = b8 + lane; i < b; i += kScanThreads) element(sg, i, count);
     const int64_t ng = (b8 - a8) / kVec;
     const char* src = static_cast<const char*>(sg.grad) + (a8 - sg.begin) * G::kBytes;
     int64_t j = lane;
-    for (; j + kThreads < ng; j += 2 * kThreads) {   // two groups in flight per lane
+    for (; j + kScanThreads < ng; j += 2 * kScanThreads) {   // two groups in flight per lane
       uint32_t w0[kVec * G::kBytes / 4], w1[kVec * G::kBytes / 4];
       load_words<G>(src + j * (kVec * G::kBytes), w0);
-      load_words<G>(src + (j + kThreads) * (kVec * G::kBytes), w1);
+      load_words<G>(src + (j + kScanThreads) * (kVec * G::kBytes), w1);
       group(sg, w0, a8 + j * kVec, count);
-      group(sg, w1, a8 + (j + kThreads) * kVec, count);
+      group(sg, w1, a8 + (j + kScanThreads) * kVec, count);
     }
     if (j < ng) {
       uint32_t w0[kVec * G::kBytes / 4];
@@ -314,7 +315,7 @@ struct GradScan {
 };
 
 template <class G, bool kFlat, bool kStats>
-__global__ __launch_bounds__(kThreads) void k_grad_stats(
+__global__ __launch_bounds__(kScanThreads) void k_grad_stats(
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
     int64_t end, int64_t own_begin, int64_t own_end, int umode,
     float grad_scale, float inv_scale, float* __restrict__ flat,
@@ -350,8 +351,9 @@ __global__ __launch_bounds__(kThreads) void k_grad_stats(
   }
   if (kStats) {
     const bool bad = sc.bad || (sc.packed & G::kTop) != 0;
-    __shared__ double wsum[kWaves];
-    __shared__ uint32_t wbad[kWaves];
+    constexpr int kScanWaves = kScanThreads / 64;
+    __shared__ double wsum[kScanWaves];
+    __shared__ uint32_t wbad[kScanWaves];
     const double w = wave_sum(sc.acc);
     const bool wb = __any(bad);
     if ((lane & 63) == 0) {
@@ -363,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void k_grad_stats(
       double total = 0.0;
       uint32_t flag = 0;
 #pragma unroll
-      for (int k = 0; k < kWaves; ++k) {
+      for (int k = 0; k < kScanWaves; ++k) {
         total += wsum[k];
         flag |= wbad[k];
       }
@@ -670,7 +672,7 @@ void launch_stats(const ms_segment_t* segs, int nseg, int64_t begin,
   const bool stats = bsum != nullptr;
   float inv = 1.0f;
   const int umode = unscale_mode(unscale, scale, &inv);
-  const dim3 block(kThreads);
+  const dim3 block(kScanThreads);
   if (stats) {
     const dim3 grid(kStatsBlocks);
     if (flat)

@@ -392,7 +392,7 @@ class FlatParamGroup:
         the tensors behind them, which the caller keeps alive until the
         kernels reading them have run."""
         dtype = self.model_dtype()
-        dev = self.device
+        index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         ptrs: List[int] = []
         keep: List[torch.Tensor] = []
         for p, n in zip(self.params, self._numels):
@@ -400,7 +400,9 @@ class FlatParamGroup:
             if g is None:
                 ptrs.append(0)
                 continue
-            if g.dtype != dtype or g.numel() != n or g.device != dev or not g.is_contiguous():
+            # dtypes are singletons; get_device() is -1 for host tensors
+            if g.dtype is not dtype or g.numel() != n or g.get_device() != index \
+                    or not g.is_contiguous():
                 g = self._check_grad(g, n, dtype)
             ptrs.append(g.data_ptr())
             keep.append(g)
@@ -422,7 +424,9 @@ class FlatParamGroup:
         with full-size parameters the rows are static and only the two
         pointer columns are filled in."""
         n_params = len(self.params)
-        full = all(p.numel() == n for p, n in zip(self.params, self._numels)) if mptrs else True
+        full = True
+        if mptrs is not None and self._partitioned:   # ZeRO-3 placeholders may be slices
+            full = all(p.numel() == n for p, n in zip(self.params, self._numels))
         if lo == 0 and hi == self.numel_padded and full:
             if self._rows is None:
                 rows, idx = [], []

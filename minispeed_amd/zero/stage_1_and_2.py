@@ -98,26 +98,28 @@ class ZeROOptimizer:
         """
         ws = self._ws()
         keep: List[torch.Tensor] = []
-        grads = []
-        for g in self.flat_groups:
-            ptrs, tensors = g.grad_pointers()
-            grads.append(ptrs)
-            keep.extend(tensors)
-            g.release_grads()
-        models = self._model_targets()
         launches = []
-        for g, group, state, gptrs, mptrs in zip(
-            self.flat_groups, self.adam.param_groups, self.adam.state, grads, models
-        ):
+        for g, group, state in zip(self.flat_groups, self.adam.param_groups, self.adam.state):
+            ptrs, tensors = g.grad_pointers()
+            keep.extend(tensors)
             lr, betas, eps, wd = FlatAdam.hyper(group)
             launches.append(GroupLaunch(
                 group=g, lr=lr, betas=betas, eps=eps, weight_decay=wd,
                 step=state["step"] + 1, exp_avg=state["exp_avg"], exp_avg_sq=state["exp_avg_sq"],
-                grads=gptrs, model=mptrs,
+                grads=ptrs,
             ))
+
+        def model_targets():
+            # runs while K1 is on the device: release param.grad (flat.py:213)
+            # and collect the cast targets
+            for g in self.flat_groups:
+                g.release_grads()
+            return self._model_targets()
+
         scalars = run_boundary(
             launches, ws, scaler=scaler, max_norm=max_norm,
-            materialize_flat_grad=materialize_flat_grad, timer=self.launch_timer,
+            materialize_flat_grad=materialize_flat_grad, model_targets=model_targets,
+            timer=self.launch_timer,
         )
         del keep  # the read-back synchronised the stream
         overflow = bool(scalars.overflow)
