@@ -140,3 +140,18 @@ def k4(table: Table, mdtype, flat: torch.Tensor, begin, end):
 
 
 __all__ = [name for name in dir() if not name.startswith("_")] + ["adamw_params"]
+
+
+def master_step_within_ulps(before, got, want, ulps=2.0):
+    """Per-step master check: |got - want| <= ulps * spacing of the largest
+    operand of the final addition p + u (p_before, the update u = want -
+    before, and the result).  Returns (ok, worst ratio)."""
+    before = np.asarray(before, dtype=np.float32)
+    got = np.asarray(got, dtype=np.float32)
+    want = np.asarray(want, dtype=np.float32)
+    upd = np.abs(want.astype(np.float64) - before.astype(np.float64)).astype(np.float32)
+    scale = np.maximum(np.maximum(np.abs(before), np.abs(want)), upd)
+    diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    ratio = diff / np.spacing(scale).astype(np.float64)
+    worst = float(ratio.max()) if ratio.size else 0.0
+    return worst <= ulps, worst

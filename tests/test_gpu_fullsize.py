@@ -1,0 +1,236 @@
+"""Parity at the benchmark workloads' real sizes.
+
+* GPT-2-small buffer (124,439,808 params, 148 tensors), fp16 grads
+  N(0,1e-3)*2^16, ZeRO-2, clip 1.0: each of the first steps checked against
+  the oracle started from the GPU's state, then 100 boundaries with fresh
+  seeded gradients against the oracle run alongside (1e-5 relative).
+* 350M buffer (292 tensors), fp16, dynamic scale 2^16 with window 1000,
+  inf/nan at 1-16 seeded positions of every 4th step for 200 steps: the
+  skip / halve trajectory is bit-exact against the reference state machine
+  and the masters, moments and model copy are untouched by skipped steps.
+* 1.3B buffer (292 tensors), bf16 grads accumulated over 4 micro-batches by
+  torch bf16 adds, ZeRO-1, WarmupDecayLR: the norm against a float64 sum of
+  squares, a random million elements bit-exact against the kernel recipe,
+  the fused and the materialized-flat-grad modes bitwise identical, two runs
+  bitwise identical.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import minispeed_amd as ms
+from minispeed_amd.workloads import shapes_of
+from oracle import boundary as ob
+from oracle import recipe
+from tests.helpers import master_step_within_ulps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _cfg(dtype, stage, *, clip=1.0, power=16, window=1000, sched=None, materialize=False, gas=1):
+    cfg = {"train_micro_batch_size_per_gpu": 1, "gradient_accumulation_steps": gas,
+           "gradient_clipping": clip, "dtype": dtype,
+           "optimizer": {"type": "AdamW", "params": {"lr": 1e-3, "betas": [0.9, 0.999],
+                                                      "eps": 1e-8, "weight_decay": 0.01}},
+           "scheduler": sched or {"type": "WarmupLR", "params": {"warmup_num_steps": 0}},
+           "zero_optimization": {"stage": stage}, "steps_per_print": 10 ** 9,
+           "hip_boundary": {"materialize_flat_grad": materialize}}
+    if dtype == "fp16":
+        cfg["fp16"] = {"enabled": True, "loss_scale": 0, "initial_scale_power": power,
+                       "loss_scale_window": window}
+    return cfg
+
+
+def _params(shapes, seed):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    return [nn.Parameter(torch.randn(*s, generator=gen, device=DEV) * 0.02) for s in shapes]
+
+
+def _engine(shapes, cfg, seed=0):
+    params = _params(shapes, seed)
+    mod = nn.ParameterList(params)
+    return ms.initialize(model=mod, model_parameters=list(mod), config=cfg), params
+
+
+def _grads(shapes, dtype, gen, scale=1.0, std=1e-3):
+    return [(torch.randn(*s, generator=gen, device=DEV) * (std * scale)).to(dtype) for s in shapes]
+
+
+def test_gpt2_small_fp16_zero2_against_oracle():
+    shapes = shapes_of("gpt2-124m")
+    engine, params = _engine(shapes, _cfg("fp16", 2))
+    ref_params = [nn.Parameter(p.detach().cpu().clone()) for p in params]
+    ref = ob.Engine([ref_params], [{"lr": 1e-3, "betas": (0.9, 0.999), "eps": 1e-8,
+                                    "weight_decay": 0.01}],
+                    dtype="fp16", zero_stage=2, clip=1.0, initial_scale_power=16,
+                    scheduler="WarmupLR", scheduler_params={"warmup_max_lr": 1e-3})
+    gen = torch.Generator(device=DEV).manual_seed(42)
+    g = engine.flat_groups[0]
+    for step in range(100):
+        before = g.data.detach().cpu() if step < 3 else None
+        if step < 3:      # per-step check from the GPU's own state
+            st = engine.optimizer.state[0]
+            ref.load_state([before], [st["exp_avg"].cpu()], [st["exp_avg_sq"].cpu()], [st["step"]],
+                           (engine.loss_scaler.scale, engine.loss_scaler.good_steps,
+                            engine.loss_scaler.skipped_steps),
+                           engine.lr_scheduler.last_epoch,
+                           [pg["lr"] for pg in engine.optimizer.param_groups])
+        grads = _grads(shapes, torch.float16, gen, scale=engine.loss_scaler.scale)
+        for p, rp, gr in zip(params, ref_params, grads):
+            p.grad = gr
+            rp.grad = gr.cpu()
+        engine.micro_steps += 1
+        ref.micro_steps += 1
+        assert engine.step() is True and ref.step() is True
+        assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
+        assert engine.loss_scaler.scale == ref.scaler.scale
+        if step < 3:
+            got = g.data.detach().cpu().numpy()
+            want = ref.groups[0].data.numpy()
+            _, _, coef = recipe.clip_coef(np.float32(ref.grad_norm), 1.0)
+            same = np.float32(engine.last_boundary.coef) == np.float32(coef)
+            ok, worst = master_step_within_ulps(before.numpy(), got, want, 2.0 if same else 4.0)
+            assert ok, (step, worst)
+            if same:
+                np.testing.assert_array_equal(engine.optimizer.state[0]["exp_avg_sq"].cpu().numpy(),
+                                              ref.state[0]["exp_avg_sq"].numpy())
+    for got, want in ((g.data, ref.groups[0].data),
+                      (engine.optimizer.state[0]["exp_avg"], ref.state[0]["exp_avg"]),
+                      (engine.optimizer.state[0]["exp_avg_sq"], ref.state[0]["exp_avg_sq"])):
+        got = got.detach().cpu().numpy()
+        want = want.numpy()
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6 * float(np.abs(want).max()))
+    assert engine.global_steps == 100 and not g.grad_shard.any()
+
+
+def test_overflow_stress_350m_trajectory():
+    shapes = shapes_of("gpt-350m")
+    engine, params = _engine(shapes, _cfg("fp16", 0))
+    sizes = [int(np.prod(s)) for s in shapes]
+    rng = np.random.default_rng(1234)
+    scaler = ob.LossScaler(True, 0.0, 1000)
+    scaler.set_scale_from_power(16)
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    g = engine.flat_groups[0]
+    specials = [float("inf"), float("-inf"), float("nan")]
+    skipped = 0
+    for step in range(200):
+        grads = _grads(shapes, torch.float16, gen, scale=engine.loss_scaler.scale)
+        inject = step % 4 == 3
+        if inject:
+            for _ in range(int(rng.integers(1, 17))):
+                ti = int(rng.integers(0, len(shapes)))
+                grads[ti].view(-1)[int(rng.integers(0, sizes[ti]))] = specials[int(rng.integers(0, 3))]
+            state0 = (g.data.clone(), engine.optimizer.state[0]["exp_avg"].clone(),
+                      engine.optimizer.state[0]["exp_avg_sq"].clone(), params[5].detach().clone())
+        for p, gr in zip(params, grads):
+            p.grad = gr
+        engine.micro_steps += 1
+        applied = engine.step()
+        scaler.update(overflow=inject)
+        skipped += inject
+        assert applied == (not inject), step
+        assert (engine.loss_scaler.scale, engine.loss_scaler.good_steps,
+                engine.loss_scaler.skipped_steps) == (scaler.scale, scaler.good_steps,
+                                                      scaler.skipped_steps), step
+        if inject:
+            assert torch.equal(g.data, state0[0])
+            assert torch.equal(engine.optimizer.state[0]["exp_avg"], state0[1])
+            assert torch.equal(engine.optimizer.state[0]["exp_avg_sq"], state0[2])
+            assert torch.equal(params[5].detach(), state0[3])
+    assert engine.skipped_steps == skipped == 50
+    assert engine.global_steps == 150 and engine.loss_scaler.scale == 1.0
+
+
+def _bf16_gas4_grads(shapes, seed):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    acc = None
+    for _ in range(4):
+        micro = _grads(shapes, torch.bfloat16, gen, std=1e-3)
+        if acc is None:
+            acc = micro
+        else:
+            for a, m in zip(acc, micro):
+                a.add_(m)              # autograd's accumulation into .grad (bf16)
+    return acc
+
+
+def test_1p3b_bf16_gas4_norm_sampled_elements_and_modes():
+    shapes = shapes_of("gpt-1.3b")
+    sched = {"type": "WarmupDecayLR", "params": {"warmup_min_lr": 0.0, "warmup_max_lr": 1e-3,
+                                                  "warmup_num_steps": 100, "total_num_steps": 1000}}
+    engine, params = _engine(shapes, _cfg("bf16", 1, sched=sched, gas=4), seed=3)
+    g = engine.flat_groups[0]
+    n = g.numel
+    offsets = np.array(g.layout.offsets, dtype=np.int64)
+    rng = np.random.default_rng(0)
+    idx = np.unique(rng.integers(0, n, size=1_000_000))
+    pi = np.searchsorted(offsets, idx, side="right") - 1
+    local = idx - offsets[pi]
+    idx_t = torch.from_numpy(idx).to(DEV)
+
+    def gather(tensors):
+        """flat values of a ragged list at the sampled indices, on the CPU"""
+        out = np.empty(len(idx), dtype=np.float32)
+        for k in np.unique(pi):
+            sel = np.nonzero(pi == k)[0]
+            t = tensors[k].detach().reshape(-1)
+            out[sel] = t[torch.from_numpy(local[sel]).to(DEV)].float().cpu().numpy()
+        return out
+
+    for step in range(2):
+        grads = _bf16_gas4_grads(shapes, seed=10 + step)
+        p0 = g.data[idx_t].cpu().numpy()
+        m0 = engine.optimizer.state[0]["exp_avg"][idx_t].cpu().numpy()
+        v0 = engine.optimizer.state[0]["exp_avg_sq"][idx_t].cpu().numpy()
+        g_s = gather(grads)
+        exact = sum(float(t.double().pow(2).sum()) for t in grads)
+        lr = engine.optimizer.param_groups[0]["lr"]
+        t_adam = engine.optimizer.state[0]["step"] + 1
+        for p, gr in zip(params, grads):
+            p.grad = gr
+        engine.micro_steps += 4
+        assert engine.step() is True
+        sc = engine.last_boundary
+        assert abs(int(np.float32(sc.sumsq).view(np.int32)) - int(np.float32(exact).view(np.int32))) <= 1
+        assert abs(engine.grad_norm - np.sqrt(exact)) <= 1e-6 * np.sqrt(exact)
+        assert sc.clip_applied == 1
+        wp, wm, wv = recipe.adamw_step(p0, m0, v0, g_s, lr=lr, betas=(0.9, 0.999), eps=1e-8,
+                                       wd=0.01, step=t_adam, clip_coef=float(np.float32(sc.coef)))
+        np.testing.assert_array_equal(g.data[idx_t].cpu().numpy().view(np.int32), wp.view(np.int32))
+        np.testing.assert_array_equal(engine.optimizer.state[0]["exp_avg"][idx_t].cpu().numpy(), wm)
+        np.testing.assert_array_equal(engine.optimizer.state[0]["exp_avg_sq"][idx_t].cpu().numpy(), wv)
+        model = gather(params)
+        np.testing.assert_array_equal(model, torch.from_numpy(wp).to(torch.bfloat16).float().numpy())
+        del grads
+
+    # fused vs materialized flat grad, and run-to-run determinism, from one state
+    state = (g.data.clone(), engine.optimizer.state[0]["exp_avg"].clone(),
+             engine.optimizer.state[0]["exp_avg_sq"].clone())
+    lr0, epoch0 = engine.optimizer.param_groups[0]["lr"], engine.lr_scheduler.last_epoch
+    results = []
+    for materialize in (False, True, False):
+        engine.config.materialize_flat_grad = materialize
+        g.data.copy_(state[0])
+        engine.optimizer.state[0]["exp_avg"].copy_(state[1])
+        engine.optimizer.state[0]["exp_avg_sq"].copy_(state[2])
+        engine.optimizer.state[0]["step"] = 2
+        engine.optimizer.param_groups[0]["lr"] = lr0      # the schedule advances per step
+        engine.lr_scheduler.last_epoch = epoch0
+        for p, gr in zip(params, _bf16_gas4_grads(shapes, seed=99)):
+            p.grad = gr
+        engine.micro_steps += 4
+        assert engine.step() is True
+        results.append((engine.last_boundary.sumsq, g.data.clone(),
+                        engine.optimizer.state[0]["exp_avg_sq"].clone(), params[7].detach().clone()))
+        if materialize:
+            assert not g.grad.any()
+    for other in results[1:]:
+        assert other[0] == results[0][0]
+        assert torch.equal(other[1], results[0][1]) and torch.equal(other[2], results[0][2])
+        assert torch.equal(other[3].view(torch.int16), results[0][3].view(torch.int16))

@@ -20,7 +20,8 @@ from minispeed_amd import _native
 from oracle import boundary as ob
 from oracle import recipe
 from tests.helpers import (DEV, HALF_SPECIALS, Table, adamw_params, bits, k1, k2, k3, k4,
-                           layout_for, ragged_grads, scalars_device, set_bits, store)
+                           layout_for, master_step_within_ulps, ragged_grads, scalars_device,
+                           set_bits, store)
 
 pytestmark = pytest.mark.gpu
 
@@ -219,9 +220,8 @@ def test_k3_against_torch_restatement(gdtype):
     ob.adam_update(tp, tg, tm, tv, lr, betas, eps, wd, step)
     np.testing.assert_array_equal(dm.cpu().numpy(), tm.numpy())
     np.testing.assert_array_equal(dv.cpu().numpy(), tv.numpy())
-    got = dp.cpu().numpy()
-    scale = np.maximum(np.abs(p), np.abs(tp.numpy()))
-    assert np.all(np.abs(got.astype(np.float64) - tp.numpy()) <= 2 * np.spacing(scale))
+    ok, worst = master_step_within_ulps(p, dp.cpu().numpy(), tp.numpy())
+    assert ok, worst
 
 
 def test_k3_skips_everything_on_overflow():
