@@ -1,6 +1,6 @@
 """Boundary-step throughput of minispeed_amd on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload gpt-1.3b]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload gpt-1.3b | llama3-8b-shard]
                     [--grad-dtype fp16] [--mode fused|materialize]
                     [--no-cpu-baseline] [--copy-calibration]
 
@@ -145,6 +145,144 @@ def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
     }
 
 
+def bench_llama_shard(args) -> dict:
+    """One rank's 1/8 ZeRO-3 shard of Llama-3-8B (rank 3 of 8) plus the full
+    cast-on-gather, at component level through the C ABI.
+
+    The shard step runs K1 -> K2 -> K3 over the owned flat range with the
+    reduce-scattered bf16 gradient pieces of every tensor that intersects it
+    (ragged views of one buffer) and bf16 placeholders as cast targets; the
+    gather casts a full fp32 master buffer into the 291 full-shaped bf16
+    parameters (K4)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from minispeed_amd import _native
+    from minispeed_amd.boundary import LaunchTimer, adamw_params
+    from minispeed_amd.flat import FlatLayout, check_table
+    from minispeed_amd.workloads import shapes_of
+
+    lib = _native.load()
+    dev = torch.device("cuda", 0)
+    stream = _native.stream_handle(dev)
+    shapes = shapes_of("llama3-8b")
+    numels = [int(np.prod(s)) for s in shapes]
+    lay = FlatLayout(numels, rank=3, world_size=8, zero_stage=3)
+    lo, hi = lay.shard_start, lay.shard_end
+    S, N = hi - lo, lay.numel_padded
+    log(f"[bench] llama3-8b: {len(shapes)} tensors, {N:,} params; rank 3 of 8 owns [{lo:,}, {hi:,})")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    grad = (torch.randn(S, generator=gen, device=dev) * 1e-4).to(torch.bfloat16)
+    holder = torch.empty(S, dtype=torch.bfloat16, device=dev)
+    master = torch.randn(S, generator=gen, device=dev) * 0.02
+    m = torch.zeros(S, device=dev)
+    v = torch.zeros(S, device=dev)
+    gs, ms_ = [], []
+    for off, n in zip(lay.offsets, numels):
+        a, b = max(off, lo), min(off + n, hi)
+        if b > a:
+            gs.append((grad.data_ptr() + (a - lo) * 2, (a, b), 2))
+            ms_.append((holder.data_ptr() + (a - lo) * 2, (a, b), 2))
+        else:
+            gs.append(None)
+            ms_.append(None)
+    table = lay.segments(lo, hi, gs, ms_)
+    check_table(table, lo, hi)
+    tdev = torch.from_numpy(table).to(dev)
+    nb = _native.stats_blocks()
+    psum = torch.empty(nb, dtype=torch.float64, device=dev)
+    pflag = torch.empty(nb, dtype=torch.int32, device=dev)
+    scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=dev)
+    host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
+    timer = LaunchTimer()
+
+    def step(k: int, timed: bool) -> None:
+        t = timer if timed else None
+        hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, k + 1)
+        tok = t.start("k1") if t else None
+        _native.check(lib.ms_grad_stats(tdev.data_ptr(), len(table), _native.DTYPE_BF16, lo, hi,
+                                        lo, hi, 0, 1.0, None, psum.data_ptr(), pflag.data_ptr(),
+                                        nb, stream), "ms_grad_stats")
+        if t:
+            t.stop(tok)
+        _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 1.0, 0, 1.0,
+                                       0, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), stream),
+                      "ms_norm_clip")
+        tok = t.start("k3") if t else None
+        _native.check(lib.ms_fused_adamw(master.data_ptr(), m.data_ptr(), v.data_ptr(), None,
+                                         tdev.data_ptr(), len(table), _native.DTYPE_BF16,
+                                         _native.DTYPE_BF16, lo, hi, ctypes.byref(hp),
+                                         scal.data_ptr(), stream), "ms_fused_adamw")
+        if t:
+            t.stop(tok)
+        host.copy_(scal, non_blocking=True)
+        torch.cuda.current_stream(dev).synchronize()
+
+    for k in range(args.warmup):
+        step(k, False)
+    step_s = []
+    for k in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step(args.warmup + k, True)
+        step_s.append(time.perf_counter() - t0)
+    res = _native.StepScalars.from_buffer_copy(host.numpy().tobytes())
+    # norm = sqrt(S * 1e-8) ~ 3.2 > clip 1.0: the clip path is exercised
+    if res.overflow or not res.clip_applied:
+        raise RuntimeError(f"unexpected step scalars: overflow={res.overflow} clip={res.clip_applied}")
+
+    # cast-on-gather of the full model: fp32 masters (all ranks' shards) -> bf16 params
+    del grad, holder
+    full = torch.randn(N, generator=gen, device=dev) * 0.02
+    params16 = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    gtable = lay.segments(0, N, [None] * len(numels),
+                          [(params16.data_ptr() + off * 2, (off, off + n), 2)
+                           for off, n in zip(lay.offsets, numels)])
+    check_table(gtable, 0, N)
+    gdev = torch.from_numpy(gtable).to(dev)
+    cast_ms = []
+    for k in range(3 + args.steps):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        _native.check(lib.ms_cast_to_model(full.data_ptr(), 0, N, gdev.data_ptr(), len(gtable),
+                                           _native.DTYPE_BF16, stream), "ms_cast_to_model")
+        ev1.record()
+        torch.cuda.synchronize()
+        if k >= 3:
+            cast_ms.append(ev0.elapsed_time(ev1))
+    sample = torch.randint(0, N, (1 << 20,), device=dev)
+    assert torch.equal(params16[sample], full[sample].to(torch.bfloat16))
+
+    ms_step = float(np.mean(step_s)) * 1e3
+    k3 = float(np.mean(timer.durations_ms("k3")))
+    cast = float(np.mean(cast_ms))
+    return {
+        "metric": "Llama-3-8B 1/8 ZeRO-3 shard boundary step + full bf16 cast-on-gather, 1 GPU",
+        "value": round(S / (ms_step * 1e-3) / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: bf16 grads N(0,1e-4), fp32 masters N(0,0.02)",
+        "config": {"workload": "one rank's 1/8 shard of Llama-3-8B (rank 3 of 8, fused mode)",
+                   "shard_params": S, "model_params": N, "tensors": len(shapes),
+                   "shard_segments": len(table), "bytes_per_param": 30},
+        "hbm_gbps": round(30 * S / (ms_step * 1e-3) / 1e9, 1),
+        "kernel_ms": {"k1": round(float(np.mean(timer.durations_ms("k1"))), 4), "k3": round(k3, 4),
+                      "cast_on_gather": round(cast, 4)},
+        "roofline": {"kernel": "K3 k_adamw (fused AdamW + placeholder cast)", "bound": "hbm",
+                     "achieved": round(28 * S / (k3 * 1e-3) / 1e9, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(28 * S / (k3 * 1e-3) / 1e9 / PEAK_GBPS, 4),
+                     "traffic": None, "bytes_per_param": 28},
+        "cast_on_gather": {"ms": round(cast, 4), "params": N, "bytes_per_param": 6,
+                           "gbps": round(6 * N / (cast * 1e-3) / 1e9, 1)},
+        "cpu_baseline": None,
+    }
+
+
 def traffic_for(kernel: str, workload: str, grad_dtype: str, mode: str):
     """HBM bytes per launch measured by rocprofv3 counters (profiles/traffic.json)."""
     try:
@@ -173,6 +311,10 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}))
         return 1
+    if args.workload == "llama3-8b-shard":
+        torch.cuda.set_device(0)
+        print(json.dumps(bench_llama_shard(args)), flush=True)
+        return 0
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     shapes = shapes_of(args.workload)

@@ -234,3 +234,78 @@ def test_1p3b_bf16_gas4_norm_sampled_elements_and_modes():
         assert other[0] == results[0][0]
         assert torch.equal(other[1], results[0][1]) and torch.equal(other[2], results[0][2])
         assert torch.equal(other[3].view(torch.int16), results[0][3].view(torch.int16))
+
+
+def test_one_rank_shard_step_and_cast_on_gather():
+    """One rank's 1/8 ZeRO-3 share (rank 5 of 8) of the GPT-2-small list at
+    component level: K1 -> K2 -> K3 over the owned range with ragged bf16
+    gradient pieces and placeholder cast targets, every element against the
+    kernel recipe; then the cast-on-gather of a full fp32 buffer into the
+    full-shaped parameters, bit-exact against round-to-nearest-even."""
+    import ctypes
+
+    from minispeed_amd import _native
+    from minispeed_amd.boundary import adamw_params
+    from minispeed_amd.flat import FlatLayout, check_table
+
+    lib = _native.load()
+    shapes = shapes_of("gpt2-124m")
+    numels = [int(np.prod(s)) for s in shapes]
+    lay = FlatLayout(numels, rank=5, world_size=8, zero_stage=3)
+    lo, hi = lay.shard_start, lay.shard_end
+    S, N = hi - lo, lay.numel_padded
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    grad = (torch.randn(S, generator=gen, device=DEV) * 1e-4).to(torch.bfloat16)
+    holder = torch.zeros(S, dtype=torch.bfloat16, device=DEV)
+    master = torch.randn(S, generator=gen, device=DEV) * 0.02
+    m = torch.randn(S, generator=gen, device=DEV) * 1e-5
+    v = torch.rand(S, generator=gen, device=DEV) * 1e-9
+    p0, m0, v0, g0 = (t.cpu().numpy().copy() for t in (master, m, v, grad.float()))
+    gs, ms_ = [], []
+    for off, n in zip(lay.offsets, numels):
+        a, b = max(off, lo), min(off + n, hi)
+        gs.append((grad.data_ptr() + (a - lo) * 2, (a, b), 2) if b > a else None)
+        ms_.append((holder.data_ptr() + (a - lo) * 2, (a, b), 2) if b > a else None)
+    table = lay.segments(lo, hi, gs, ms_)
+    check_table(table, lo, hi)
+    tdev = torch.from_numpy(table).to(DEV)
+    nb = _native.stats_blocks()
+    psum = torch.empty(nb, dtype=torch.float64, device=DEV)
+    pflag = torch.empty(nb, dtype=torch.int32, device=DEV)
+    scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
+    st = _native.stream_handle(torch.device(DEV))
+    _native.check(lib.ms_grad_stats(tdev.data_ptr(), len(table), _native.DTYPE_BF16, lo, hi, lo, hi,
+                                    0, 1.0, None, psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
+    _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 0.05, 0, 1.0, 0, 0,
+                                   1000, 1.0, 2.0 ** 24, scal.data_ptr(), st), "k2")
+    hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 4)
+    _native.check(lib.ms_fused_adamw(master.data_ptr(), m.data_ptr(), v.data_ptr(), None,
+                                     tdev.data_ptr(), len(table), _native.DTYPE_BF16,
+                                     _native.DTYPE_BF16, lo, hi, ctypes.byref(hp),
+                                     scal.data_ptr(), st), "k3")
+    torch.cuda.synchronize()
+    sc = _native.StepScalars.from_buffer_copy(scal.cpu().numpy().tobytes())
+    exact = recipe.sumsq_f64(g0)
+    assert not sc.overflow and sc.clip_applied
+    assert abs(int(np.float32(sc.sumsq).view(np.int32)) - int(np.float32(exact).view(np.int32))) <= 1
+    wp, wm, wv = recipe.adamw_step(p0, m0, v0, g0, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, wd=0.01,
+                                   step=4, clip_coef=float(np.float32(sc.coef)))
+    np.testing.assert_array_equal(master.cpu().numpy().view(np.int32), wp.view(np.int32))
+    np.testing.assert_array_equal(m.cpu().numpy().view(np.int32), wm.view(np.int32))
+    np.testing.assert_array_equal(v.cpu().numpy().view(np.int32), wv.view(np.int32))
+    assert torch.equal(holder.view(torch.int16),
+                       torch.from_numpy(wp).to(torch.bfloat16).to(DEV).view(torch.int16))
+
+    full = torch.randn(N, generator=gen, device=DEV) * 0.02
+    full[:5] = torch.tensor([3.0e38, -1e-40, 0.0, -0.0, 1.00390625], device=DEV)
+    params16 = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shapes]
+    gtable = lay.segments(0, N, [None] * len(numels),
+                          [(t.data_ptr(), (off, off + t.numel()), 2) for t, off in zip(params16, lay.offsets)])
+    check_table(gtable, 0, N)
+    gdev = torch.from_numpy(gtable).to(DEV)
+    _native.check(lib.ms_cast_to_model(full.data_ptr(), 0, N, gdev.data_ptr(), len(gtable),
+                                       _native.DTYPE_BF16, st), "k4")
+    torch.cuda.synchronize()
+    want = full[:lay.numel].to(torch.bfloat16)
+    got = torch.cat([t.reshape(-1) for t in params16])
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
