@@ -174,7 +174,7 @@ def run_boundary(
     dtypes, flats = [], []
     for gi, gl in enumerate(launches):
         g = gl.group
-        dtype = _native.ms_dtype(g.model_dtype())
+        dtype = _native.ms_dtype(g.params[0].dtype)
         flat_out = None
         if materialize_flat_grad:
             if g.grad is None:

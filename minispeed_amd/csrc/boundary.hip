@@ -39,8 +39,9 @@ constexpr int kThreads = 256;             // 4 wave64 per block
 constexpr int kWaves = kThreads / 64;
 constexpr int kVec = 8;                   // elements per lane per tile
 constexpr int kTile = kThreads * kVec;    // 2048 flat elements
-constexpr int kStatsBlocks = 4096;        // fixed K1 grid (determinism)
+constexpr int kStatsBlocks = 16384;       // fixed K1 grid (determinism)
 constexpr int kScanThreads = 512;         // K1 block: 8 wave64
+constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
 constexpr int kMaxSegs = 1 << 26;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -380,13 +381,14 @@ __global__ __launch_bounds__(kScanThreads) void k_grad_stats(
 }
 
 // ------------------------------------------------------------------ K2
-__global__ __launch_bounds__(kThreads) void k_norm_clip(
+__global__ __launch_bounds__(kNormThreads) void k_norm_clip(
     const double* __restrict__ bsum, const uint32_t* __restrict__ bflag,
     int nblk, int ngroups, int has_clip, double max_norm, int scaler_enabled,
     double scale, int64_t good_steps, int64_t skipped_steps, int64_t window,
     double min_scale, double max_scale, ms_step_scalars_t* __restrict__ out) {
-  __shared__ double wsum[kWaves];
-  __shared__ uint32_t wbad[kWaves];
+  constexpr int kNormWaves = kNormThreads / 64;
+  __shared__ double wsum[kNormWaves];
+  __shared__ uint32_t wbad[kNormWaves];
   const int tid = threadIdx.x;
   float total = 0.0f;      // meaningful in thread 0
   uint32_t overflow = 0;   // meaningful in thread 0
@@ -395,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_clip(
     const uint32_t* pf = bflag + static_cast<int64_t>(gi) * nblk;
     double acc = 0.0;
     uint32_t bad = 0;
-    for (int b = tid; b < nblk; b += kThreads) {
+    for (int b = tid; b < nblk; b += kNormThreads) {
       acc += ps[b];
       bad |= pf[b];
     }
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_clip(
     __syncthreads();
     if (tid == 0) {
       double gsum = 0.0;
-      for (int k = 0; k < kWaves; ++k) {
+      for (int k = 0; k < kNormWaves; ++k) {
         gsum += wsum[k];
         overflow |= wbad[k];
       }
@@ -796,7 +798,7 @@ int ms_norm_clip(const double* block_sumsq, const uint32_t* block_flag,
   if (nblk < kStatsBlocks) return MS_EBLOCKS;
   if (window < 1) return MS_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_norm_clip, dim3(1), dim3(kThreads), 0, st, block_sumsq,
+  hipLaunchKernelGGL(k_norm_clip, dim3(1), dim3(kNormThreads), 0, st, block_sumsq,
                      block_flag, nblk, ngroups, has_clip, max_norm,
                      scaler_enabled, scale, good_steps, skipped_steps, window,
                      min_scale, max_scale, out);

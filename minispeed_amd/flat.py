@@ -167,33 +167,44 @@ def check_table(table: np.ndarray, lo: int, hi: int) -> None:
 
 
 class SegmentTable:
-    """Device copy of a segment table, re-uploaded only when it changes.
+    """Device copies of the last few segment tables of one purpose.
 
-    Uploads go through a fresh pinned host tensor with a non-blocking copy on
-    the current stream; torch's host allocator keeps that staging memory
-    until the copy has run, and the copy is stream-ordered before the
-    kernels that read the table.
+    A table equal to a cached one is reused without any copy (the gradient
+    addresses of consecutive windows often repeat).  A new table goes
+    through a fresh pinned host tensor with a non-blocking copy on the
+    current stream, replacing the least recently used entry; torch's host
+    allocator keeps the staging memory until the copy has run, and the copy
+    is stream-ordered before the kernels that read the table.  Entries are
+    only replaced between boundaries, which end with a stream
+    synchronisation, so no kernel still reads a replaced entry.
     """
+
+    SLOTS = 4
 
     def __init__(self, device: torch.device):
         self.device = device
-        self._host: Optional[np.ndarray] = None
-        self._dev: Optional[torch.Tensor] = None
+        self._entries: List[Tuple[np.ndarray, torch.Tensor]] = []   # most recent last
 
     def upload(self, table: np.ndarray) -> Tuple[int, int]:
         """Return (device pointer, row count)."""
         n = int(table.shape[0])
         if n == 0:
             return 0, 0
-        if self._host is not None and self._host.shape == table.shape and np.array_equal(self._host, table):
-            return self._dev.data_ptr(), n
+        for k, (host, dev) in enumerate(self._entries):
+            if host.shape == table.shape and np.array_equal(host, table):
+                self._entries.append(self._entries.pop(k))
+                return dev.data_ptr(), n
         staging = torch.empty((n, 4), dtype=torch.int64, pin_memory=True)
         staging.numpy()[:] = table
-        if self._dev is None or self._dev.shape[0] != n:
-            self._dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
-        self._dev.copy_(staging, non_blocking=True)
-        self._host = table.copy()
-        return self._dev.data_ptr(), n
+        if len(self._entries) >= self.SLOTS:
+            _, dev = self._entries.pop(0)
+            if dev.shape[0] != n:
+                dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
+        else:
+            dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
+        dev.copy_(staging, non_blocking=True)
+        self._entries.append((table.copy(), dev))
+        return dev.data_ptr(), n
 
 
 _ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
@@ -257,6 +268,7 @@ class FlatParamGroup:
         self._grad_dirty = False
         self._tables = {}
         self._rows = None   # static (begin, numel) rows of the whole-range table
+        self._device_index = device.index if device.index is not None else torch.cuda.current_device()
 
     # ------------------------------------------------------------- ranges
     @property
@@ -391,29 +403,34 @@ class FlatParamGroup:
         """Device address of every parameter's gradient (0: no gradient) and
         the tensors behind them, which the caller keeps alive until the
         kernels reading them have run."""
-        dtype = self.model_dtype()
-        index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        # every gradient is checked against the first parameter's dtype (the
+        # group's); model_pointers() checks the parameters themselves
+        dtype = self.params[0].dtype
+        index = self._device_index
         ptrs: List[int] = []
-        keep: List[torch.Tensor] = []
-        for p, n in zip(self.params, self._numels):
-            g = p.grad
+        keep = [p.grad for p in self.params]
+        for k, (g, n) in enumerate(zip(keep, self._numels)):
             if g is None:
                 ptrs.append(0)
                 continue
             # dtypes are singletons; get_device() is -1 for host tensors
             if g.dtype is not dtype or g.numel() != n or g.get_device() != index \
                     or not g.is_contiguous():
-                g = self._check_grad(g, n, dtype)
+                g = keep[k] = self._check_grad(g, n, dtype)
             ptrs.append(g.data_ptr())
-            keep.append(g)
         return ptrs, keep
 
     def model_pointers(self) -> List[int]:
-        """Device address of every parameter's storage (the cast target)."""
+        """Device address of every parameter's storage (the cast target);
+        every parameter must have the group's dtype and live on its device."""
+        dtype = self.params[0].dtype
+        index = self._device_index
         ptrs = []
         for p in self.params:
-            if not p.is_contiguous():
-                raise RuntimeError("parameter data must be contiguous")
+            if p.dtype is not dtype or p.get_device() != index or not p.is_contiguous():
+                self.model_dtype()   # raises for mixed dtypes
+                raise RuntimeError(
+                    f"parameter storage must be contiguous on {self.device}, got {p.device}")
             ptrs.append(p.data_ptr())
         return ptrs
 
