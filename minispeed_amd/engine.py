@@ -27,6 +27,7 @@ import torch
 from torch import nn
 
 from . import _native, comm
+from . import checkpoint as ckpt
 from .config import DeepSpeedConfig, load_config
 from .flat import FlatParamGroup, build_flat_groups
 from .optim import build_scheduler
@@ -260,10 +261,12 @@ class DeepSpeedEngine:
             g.copy_model_to_flat()
 
     def save_checkpoint(self, save_dir: str, tag: Optional[str] = None, **kwargs):
-        raise NotImplementedError("checkpoint save/load is not part of this build")
+        """minispeed's checkpoint layout (checkpoint.py:35-71)."""
+        return ckpt.save_checkpoint(self, save_dir, tag=tag)
 
     def load_checkpoint(self, load_dir: str, tag: Optional[str] = None, **kwargs):
-        raise NotImplementedError("checkpoint save/load is not part of this build")
+        """Resume from a checkpoint in minispeed's layout (checkpoint.py:74-125)."""
+        return ckpt.load_checkpoint(self, load_dir, tag=tag)
 
     def get_loss_scale(self) -> float:
         return self.loss_scaler.scale

@@ -16,9 +16,15 @@ Two engine-level traces (an MLP trained through autograd, fp32 and bf16,
 gas 2) record losses and parameters; they pin the host-side loss scaling and
 boundary gating as well.
 
+Three cases also write a checkpoint with minispeed's own
+``engine.save_checkpoint`` part-way through (``CHECKPOINTS``: case -> number
+of boundaries before the save) into ``ckpt/<case>/``; the trajectory after
+the save pins a resume from minispeed's files.
+
 Outputs, next to this script: ``<case>.npz`` (arrays, loaded with
-``allow_pickle=False``) and ``cases.json`` (per-case configuration and
-scalar trajectories).
+``allow_pickle=False``; rewritten only when an array changed),
+``ckpt/<case>/`` and ``cases.json`` (per-case configuration and scalar
+trajectories).
 """
 
 from __future__ import annotations
@@ -26,6 +32,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import shutil
 import sys
 
 import numpy as np
@@ -104,6 +111,9 @@ CASES = {
 }
 
 
+CHECKPOINTS = {"fp16_z2_clip": 4, "bf16_z1_noclip_2groups": 3, "fp16_z3_overflow": 3}
+
+
 def run_case(ms, name, spec, out_arrays, meta):
     torch.manual_seed(0)
     init = make_params(100, SHAPES)
@@ -152,6 +162,12 @@ def run_case(ms, name, spec, out_arrays, meta):
             "adam_step": [int(st["step"]) for st in engine.optimizer.state],
         }
         traj.append(rec)
+        if CHECKPOINTS.get(name) == step + 1:
+            ckpt_root = os.path.join(HERE, "ckpt", name)
+            shutil.rmtree(ckpt_root, ignore_errors=True)
+            ckpt_dir = engine.save_checkpoint(ckpt_root)
+            meta.setdefault("_checkpoints", {})[name] = {
+                "after_steps": step + 1, "tag": os.path.basename(ckpt_dir)}
         for gi, fg in enumerate(engine.flat_groups):
             out_arrays[f"s{step}_master{gi}"] = fg.data.numpy().copy()
             st = engine.optimizer.state[gi]
@@ -159,10 +175,13 @@ def run_case(ms, name, spec, out_arrays, meta):
             out_arrays[f"s{step}_v{gi}"] = st["exp_avg_sq"].numpy().copy()
         for i, p in enumerate(ps):
             out_arrays[f"s{step}_model{i}"] = bits(p.data)
+    ckpt = meta.pop("_checkpoints", {}).get(name)
     meta[name] = {"config": spec["cfg"], "groups": spec["groups"],
                   "group_opts": [{k: list(v) if isinstance(v, tuple) else v for k, v in o.items()}
                                  for o in (opts or [])],
                   "shapes": SHAPES, "steps": spec["steps"], "trajectory": traj}
+    if ckpt:
+        meta[name]["checkpoint"] = ckpt
 
 
 class MLP(nn.Module):
@@ -208,6 +227,20 @@ def run_mlp_trace(ms, name, dtype, out_arrays, meta, steps=4, gas=2, micro=4):
                   "global_steps": engine.global_steps}
 
 
+def save_npz(name, arrays):
+    """Write ``<name>.npz`` unless it already holds exactly these arrays
+    (the zip container stamps times, so rewriting would churn the file)."""
+    path = os.path.join(HERE, f"{name}.npz")
+    if os.path.exists(path):
+        with np.load(path, allow_pickle=False) as z:
+            same = sorted(z.files) == sorted(arrays) and all(
+                z[k].dtype == arrays[k].dtype and np.array_equal(z[k], arrays[k], equal_nan=True)
+                for k in arrays)
+        if same:
+            return
+    np.savez_compressed(path, **arrays)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--reference", default="/root/reference")
@@ -224,11 +257,11 @@ def main(argv=None):
     for name, spec in CASES.items():
         arrays = {}
         run_case(ms, name, spec, arrays, meta["cases"])
-        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **arrays)
+        save_npz(name, arrays)
     for name, dtype in (("mlp_fp32_trace", "fp32"), ("mlp_bf16_trace", "bf16")):
         arrays = {}
         run_mlp_trace(ms, name, dtype, arrays, meta["cases"])
-        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **arrays)
+        save_npz(name, arrays)
     with open(os.path.join(HERE, "cases.json"), "w", encoding="utf-8") as fh:
         json.dump(meta, fh, indent=1, sort_keys=True)
     print("wrote", sorted(meta["cases"]))

@@ -85,3 +85,20 @@ class MLP(nn.Module):
 
     def forward(self, x):
         return self.net(x)
+
+
+class Holder(nn.Module):
+    """The module of the recorded cases: a ParameterList named ``ps``, so
+    state-dict keys are ``ps.0`` ... ``ps.4`` (tests/golden/make_golden.py)."""
+
+    def __init__(self, params):
+        super().__init__()
+        self.ps = nn.ParameterList(params)
+
+
+CHECKPOINT_CASES = sorted(k for k, v in META["cases"].items() if "checkpoint" in v)
+
+
+def checkpoint_root(name: str) -> str:
+    """Directory of the checkpoint minispeed wrote part-way through a case."""
+    return os.path.join(GOLDEN_DIR, "ckpt", name)
