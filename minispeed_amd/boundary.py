@@ -74,6 +74,12 @@ class Workspace:
         self.flags = torch.empty(n, dtype=torch.int32, device=device)
         self.scalars = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=device)
         self.host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
+        # the read-back runs on a side stream (default priority) that waits
+        # for K2 only, so K3 is not queued behind the copy and the host's
+        # bookkeeping overlaps K3
+        self._side = torch.cuda.Stream(device)
+        self._k2_done = torch.cuda.Event()
+        self._copied = torch.cuda.Event()
 
     def partial_ptrs(self, g: int):
         off = g * self.nblk
@@ -86,6 +92,21 @@ class Workspace:
         """Copy K2's result to pinned memory and wait for the stream."""
         self.host.copy_(self.scalars, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
+        return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
+
+    def start_readback(self) -> None:
+        """Queue the copy of K2's scalars (just launched on the current
+        stream) to pinned memory on the side stream."""
+        self._k2_done.record(torch.cuda.current_stream(self.device))
+        self._side.wait_event(self._k2_done)
+        with torch.cuda.stream(self._side):
+            self.host.copy_(self.scalars, non_blocking=True)
+            self._copied.record(self._side)
+
+    def finish_readback(self) -> _native.StepScalars:
+        """Wait for the copy queued by :meth:`start_readback` (K2 and the
+        copy only; later kernels on the current stream keep running)."""
+        self._copied.synchronize()
         return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
 
 
@@ -157,11 +178,15 @@ def run_boundary(
 ) -> _native.StepScalars:
     """Launch the whole boundary and return K2's scalars (one host sync).
 
-    K1 and K2 are launched as soon as the gradient addresses are known;
-    ``model_targets()`` (the addresses K3 casts the updated masters into, per
-    group; ``None`` for no write) is called after that, so whatever it does
-    on the host overlaps K1 on the device.  The caller keeps the gradient
-    tensors behind ``GroupLaunch.grads`` referenced until this returns.
+    K1 and K2 are launched as soon as the gradient addresses are known and
+    the copy of K2's scalars is queued on a side stream; ``model_targets()``
+    (the addresses K3 casts the updated masters into, per group; ``None`` for
+    no write) is called after that, so whatever it does on the host overlaps
+    K1 on the device.  The function returns once K2's scalars are on the
+    host, which is before K3 has finished: K3 runs on the current stream, so
+    everything queued there afterwards is ordered after it.  The gradient
+    tensors behind ``GroupLaunch.grads`` may be dropped once this returns
+    (the caching allocator reuses their memory only in stream order).
     """
     lib = _native.load()
     device = ws.device
@@ -206,6 +231,7 @@ def run_boundary(
     )
     timer.stop(tok)
     _native.check(rc, "ms_norm_clip")
+    ws.start_readback()
 
     models = model_targets()
     for gl, dtype, flat_out, mptrs in zip(launches, dtypes, flats, models):
@@ -231,7 +257,7 @@ def run_boundary(
         timer.stop(tok)
         _native.check(rc, "ms_fused_adamw")
 
-    return ws.read_scalars()
+    return ws.finish_readback()
 
 
 # ------------------------------------------------------------------ utility

@@ -1,9 +1,14 @@
-"""Build ``libminispeed_boundary.so`` in-tree with hipcc for gfx950.
+"""Build the native parts in-tree.
 
     python -m minispeed_amd.build [--verbose]
 
-The library is a plain C-ABI shared object (no torch headers); it is written
-next to this file so that it travels with the source tree.
+* ``libminispeed_boundary.so``: the HIP kernels for gfx950 behind a plain C
+  ABI (no torch headers), compiled with hipcc;
+* ``_walk.so``: a small host-only Python extension (g++, torch and pybind11
+  headers) that collects the device addresses of parameter gradients and
+  storages for the segment tables.
+
+Both are written next to this file so that they travel with the source tree.
 """
 
 from __future__ import annotations
@@ -71,12 +76,47 @@ def build(verbose: bool = False) -> str:
     return OUTPUT
 
 
+WALK_SOURCE = os.path.join(PKG_DIR, "csrc", "walk.cpp")
+WALK_OUTPUT = os.path.join(PKG_DIR, "_walk.so")
+
+
+def walk_command(output: str = WALK_OUTPUT) -> List[str]:
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [sysconfig.get_paths()["include"], *cpp_extension.include_paths()]
+    libdir = cpp_extension.library_paths()[0]
+    return [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+            f"-D_GLIBCXX_USE_CXX11_ABI={abi}", *[f"-I{d}" for d in incs], WALK_SOURCE,
+            "-o", output, f"-L{libdir}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+
+
+def build_walk(verbose: bool = False) -> str:
+    """Compile ``_walk.so`` (always)."""
+    tmp = WALK_OUTPUT + ".tmp"
+    cmd = walk_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed ({proc.returncode}):\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, WALK_OUTPUT)
+    return WALK_OUTPUT
+
+
+def build_all(verbose: bool = False) -> List[str]:
+    return [build(verbose=verbose), build_walk(verbose=verbose)]
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--verbose", action="store_true")
     args = ap.parse_args(argv)
-    path = build(verbose=args.verbose)
-    print(path)
+    for path in build_all(verbose=args.verbose):
+        print(path)
     return 0
 
 

@@ -42,6 +42,24 @@ def _overlap(a: Range, b: Range) -> Range:
     return (lo, hi) if lo < hi else (lo, lo)
 
 
+def _walk():
+    """The C++ pointer walk (``_walk.so``, built next to this file)."""
+    try:
+        from . import _walk as mod
+    except ImportError as exc:
+        raise _native.NativeLibraryError(
+            "minispeed_amd/_walk.so is missing or does not load; build it with "
+            "`python -m minispeed_amd.build`") from exc
+    return mod
+
+
+def _with_pad_slot(ptrs, n_params: int) -> np.ndarray:
+    """Addresses as int64 with a trailing 0 for the padding row."""
+    if isinstance(ptrs, np.ndarray) and ptrs.shape == (n_params + 1,):
+        return ptrs
+    return np.asarray(list(ptrs) + [0], dtype=np.uint64).astype(np.int64)
+
+
 # --------------------------------------------------------------------------
 class FlatLayout:
     """Index math of one flat group; no device memory, CPU-testable."""
@@ -261,6 +279,7 @@ class FlatParamGroup:
         )
         self._offsets: List[Tuple[int, nn.Parameter]] = list(zip(lay.offsets, self.params))
         self._numels: List[int] = list(lay.numels)
+        self._numels_np = np.asarray(self._numels, dtype=np.int64)
         self._shapes: List[Tuple[int, ...]] = [tuple(p.shape) for p in self.params]
         self._partitioned = False
         # True while `grad` / `grad_shard` may hold non-zero values; lets
@@ -399,39 +418,46 @@ class FlatParamGroup:
             raise RuntimeError(f"gradient on {g.device}, expected {self.device}")
         return g.contiguous()
 
-    def grad_pointers(self) -> Tuple[List[int], List[torch.Tensor]]:
+    def grad_pointers(self) -> Tuple[np.ndarray, List[Optional[torch.Tensor]]]:
         """Device address of every parameter's gradient (0: no gradient) and
         the tensors behind them, which the caller keeps alive until the
-        kernels reading them have run."""
-        # every gradient is checked against the first parameter's dtype (the
-        # group's); model_pointers() checks the parameters themselves
-        dtype = self.params[0].dtype
-        index = self._device_index
-        ptrs: List[int] = []
-        keep = [p.grad for p in self.params]
-        for k, (g, n) in enumerate(zip(keep, self._numels)):
-            if g is None:
-                ptrs.append(0)
-                continue
-            # dtypes are singletons; get_device() is -1 for host tensors
-            if g.dtype is not dtype or g.numel() != n or g.get_device() != index \
-                    or not g.is_contiguous():
-                g = keep[k] = self._check_grad(g, n, dtype)
-            ptrs.append(g.data_ptr())
+        kernels reading them are queued.
+
+        The addresses are an int64 array with one extra trailing 0 (the
+        padding row's).  Every gradient is checked against the first
+        parameter's dtype (the group's), its size, device and layout; the
+        C++ walk covers the common case and this loop takes over at the first
+        gradient it does not accept (to raise, or to make a contiguous copy).
+        """
+        n_params = len(self.params)
+        ptrs = np.zeros(n_params + 1, dtype=np.int64)
+        bad, keep = _walk().grad_pointers(self.params, self._numels_np, self._device_index, ptrs)
+        if bad >= 0:
+            dtype = self.params[0].dtype
+            index = self._device_index
+            for k in range(bad, n_params):
+                g, n = self.params[k].grad, self._numels[k]
+                if g is not None:
+                    # dtypes are singletons; get_device() is -1 for host tensors
+                    if g.dtype is not dtype or g.numel() != n or g.get_device() != index \
+                            or not g.is_contiguous():
+                        g = self._check_grad(g, n, dtype)
+                    ptrs[k] = g.data_ptr()
+                keep.append(g)
         return ptrs, keep
 
-    def model_pointers(self) -> List[int]:
-        """Device address of every parameter's storage (the cast target);
-        every parameter must have the group's dtype and live on its device."""
-        dtype = self.params[0].dtype
-        index = self._device_index
-        ptrs = []
-        for p in self.params:
-            if p.dtype is not dtype or p.get_device() != index or not p.is_contiguous():
-                self.model_dtype()   # raises for mixed dtypes
-                raise RuntimeError(
-                    f"parameter storage must be contiguous on {self.device}, got {p.device}")
-            ptrs.append(p.data_ptr())
+    def model_pointers(self) -> np.ndarray:
+        """Device address of every parameter's storage (the cast target),
+        with a trailing 0 like :meth:`grad_pointers`; every parameter must
+        have the group's dtype, be contiguous and live on its device."""
+        ptrs = np.zeros(len(self.params) + 1, dtype=np.int64)
+        bad = _walk().model_pointers(self.params, self._device_index, ptrs)
+        if bad >= 0:
+            p = self.params[bad]
+            self.model_dtype()   # raises for mixed dtypes
+            raise RuntimeError(
+                f"parameter storage must be contiguous on {self.device}, got {p.device}"
+                + ("" if p.is_contiguous() else " (non-contiguous)"))
         return ptrs
 
     def boundary_table(self, lo: int, hi: int, gptrs: Optional[List[int]],
@@ -461,9 +487,9 @@ class FlatParamGroup:
             base, idx = self._rows
             table = base.copy()
             if gptrs is not None:
-                table[:, 2] = np.asarray(list(gptrs) + [0], dtype=np.uint64).astype(np.int64)[idx]
+                table[:, 2] = _with_pad_slot(gptrs, n_params)[idx]
             if mptrs is not None:
-                table[:, 3] = np.asarray(list(mptrs) + [0], dtype=np.uint64).astype(np.int64)[idx]
+                table[:, 3] = _with_pad_slot(mptrs, n_params)[idx]
             return table
         esz_g = _ELEM_BYTES[self.model_dtype()]
         grads = [None] * n_params

@@ -121,7 +121,7 @@ class ZeROOptimizer:
             materialize_flat_grad=materialize_flat_grad, model_targets=model_targets,
             timer=self.launch_timer,
         )
-        del keep  # the read-back synchronised the stream
+        del keep  # K3 may still run: freed memory is reused in stream order
         overflow = bool(scalars.overflow)
         if not overflow:
             self.grad_norm = float(scalars.norm)

@@ -114,3 +114,24 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "_lib", None)
     with pytest.raises(_native.NativeLibraryError):
         _native.load()
+
+
+def test_pointer_walk_extension_loads_and_defers_host_tensors():
+    """The C++ walk is built in-tree and hands every tensor it does not
+    accept (here: host tensors) back to the Python checks by index."""
+    import numpy as np
+    import torch
+    from torch import nn
+
+    from minispeed_amd import _walk
+
+    params = [nn.Parameter(torch.zeros(3)), nn.Parameter(torch.zeros(2))]
+    out = np.full(3, -7, dtype=np.int64)
+    bad, keep = _walk.grad_pointers(params, np.array([3, 2], dtype=np.int64), 0, out)
+    assert (bad, keep, list(out[:2])) == (-1, [None, None], [0, 0])
+    params[1].grad = torch.ones(2)
+    bad, keep = _walk.grad_pointers(params, np.array([3, 2], dtype=np.int64), 0, out)
+    assert bad == 1 and keep == [None]
+    assert _walk.model_pointers(params, 0, out) == 0
+    with pytest.raises(ValueError):
+        _walk.grad_pointers(params, np.array([3], dtype=np.int64), 0, out)
