@@ -1,7 +1,7 @@
 """Boundary-step throughput of minispeed_amd on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload gpt-1.3b | llama3-8b-shard]
-                    [--grad-dtype fp16] [--mode fused|materialize]
+                    [--grad-dtype fp16] [--mode fused|materialize] [--zero-stage 1]
                     [--no-cpu-baseline] [--copy-calibration]
 
 A step is one gradient-accumulation boundary through the engine API
@@ -64,6 +64,8 @@ def parse(argv=None):
     ap.add_argument("--workload", default="gpt-1.3b")
     ap.add_argument("--grad-dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
     ap.add_argument("--mode", default="fused", choices=["fused", "materialize"])
+    ap.add_argument("--zero-stage", type=int, default=1, choices=[0, 1, 2, 3],
+                    help="ZeRO stage at world size 1 (3: also times the parameter gather)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-params", type=int, default=50_000_000)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -71,7 +73,7 @@ def parse(argv=None):
     return ap.parse_args(argv)
 
 
-def engine_config(grad_dtype: str, mode: str) -> dict:
+def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1) -> dict:
     cfg = {
         "train_micro_batch_size_per_gpu": 1,
         "gradient_accumulation_steps": 1,
@@ -82,7 +84,7 @@ def engine_config(grad_dtype: str, mode: str) -> dict:
         "scheduler": {"type": "WarmupDecayLR",
                       "params": {"warmup_min_lr": 0.0, "warmup_max_lr": 1e-3,
                                  "warmup_num_steps": 100, "total_num_steps": 1000}},
-        "zero_optimization": {"stage": 1},
+        "zero_optimization": {"stage": zero_stage},
         "hip_boundary": {"materialize_flat_grad": mode == "materialize"},
         "steps_per_print": 1000000,
     }
@@ -327,7 +329,7 @@ def main(argv=None) -> int:
     params = [nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
     module = nn.ParameterList(params)
     engine = ms.initialize(model=module, model_parameters=list(module),
-                           config=engine_config(args.grad_dtype, args.mode))
+                           config=engine_config(args.grad_dtype, args.mode, args.zero_stage))
     mult = 2.0 ** 16 if args.grad_dtype == "fp16" else 1.0
     grad_sets = []
     for _ in range(2):
@@ -336,8 +338,17 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     log("[bench] buffers resident; warming up")
 
+    gather_s = []
+
     def attach(k: int) -> None:
-        """What the last backward of a window leaves: grads on every param."""
+        """What the last backward of a window leaves: grads on every param
+        (ZeRO-3: after the forward's parameter gather, timed on its own)."""
+        if args.zero_stage == 3:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            engine.optimizer.gather_parameters()
+            torch.cuda.synchronize()
+            gather_s.append(time.perf_counter() - t0)
         for p, g in zip(params, grad_sets[k % 2]):
             p.grad = g
         engine.micro_steps += 1
@@ -350,6 +361,7 @@ def main(argv=None) -> int:
         attach(k)
         boundary()
     torch.cuda.synchronize()
+    gather_s.clear()
     timer = LaunchTimer()
     engine.optimizer.launch_timer = timer
     step_s = []
@@ -405,7 +417,7 @@ def main(argv=None) -> int:
             "tensors": len(shapes),
             "grad_dtype": args.grad_dtype,
             "model_dtype": args.grad_dtype,
-            "zero_stage": 1,
+            "zero_stage": args.zero_stage,
             "world_size": 1,
             "mode": args.mode,
             "clip": 1.0,
@@ -426,6 +438,16 @@ def main(argv=None) -> int:
         },
         "cpu_baseline": None,
     }
+    if args.zero_stage == 3:
+        # the gather is a change of views; a stale copy would cost one cast
+        engine.optimizer.gather_parameters()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for g in engine.flat_groups:
+            g.copy_flat_to_model()
+        torch.cuda.synchronize()
+        result["zero3"] = {"gather_ms": round(float(np.mean(gather_s)) * 1e3, 4),
+                           "recast_ms": round((time.perf_counter() - t0) * 1e3, 4)}
     if not args.no_cpu_baseline:
         del grad_sets, engine, params, module
         torch.cuda.empty_cache()

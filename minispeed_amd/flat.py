@@ -282,6 +282,18 @@ class FlatParamGroup:
         self._numels_np = np.asarray(self._numels, dtype=np.int64)
         self._shapes: List[Tuple[int, ...]] = [tuple(p.shape) for p in self.params]
         self._partitioned = False
+        # ZeRO-3: the model-dtype copy of the owned shard.  Freed parameters
+        # are flat views into it; at world size 1 the gathered parameters are
+        # shaped views into it as well, so gather and free move no data.
+        self.model_shard: Optional[torch.Tensor] = None
+        self._full_model: Optional[torch.Tensor] = None   # gathered buffer, world size > 1
+        self._materialized = False
+        self._shard_views: Optional[List[torch.Tensor]] = None   # placeholders, built once
+        self._full_views: Optional[List[torch.Tensor]] = None    # gathered, world size 1
+        # (address and version of `data`, summed parameter versions) when
+        # model_shard last received the cast of `data`; None once the masters
+        # changed without that cast
+        self._model_token: Optional[Tuple[int, int, int]] = None
         # True while `grad` / `grad_shard` may hold non-zero values; lets
         # zero_grad skip clearing buffers the fused boundary never wrote.
         self._grad_dirty = False
@@ -353,6 +365,7 @@ class FlatParamGroup:
             self.data.data_ptr(), None, None, 0, _native.stream_handle(self.device),
         )
         _native.check(rc, "ms_grad_stats(flatten)")
+        self.masters_written()
 
     @torch.no_grad()
     def copy_flat_to_model(self, full_flat: Optional[torch.Tensor] = None) -> None:
@@ -366,8 +379,13 @@ class FlatParamGroup:
         _native.require_hip_tensor(buf, "flat master buffer")
         end = base + buf.numel()
         dtype = self.model_dtype()
-        stores = self.model_storages()
-        table = self.layout.segments(base, end, [None] * len(stores), stores)
+        into_shard = self._params_view_model_shard()
+        if into_shard and (base, end) == (self.shard_start, self.shard_end):
+            # the parameters tile model_shard: one contiguous segment
+            table = np.array([[base, end - base, 0, self.model_shard.data_ptr()]], dtype=np.int64)
+        else:
+            stores = self.model_storages()
+            table = self.layout.segments(base, end, [None] * len(stores), stores)
         check_table(table, base, end)
         ptr, n = self.table("to_model").upload(table)
         rc = _native.load().ms_cast_to_model(
@@ -375,33 +393,94 @@ class FlatParamGroup:
             _native.stream_handle(self.device),
         )
         _native.check(rc, "ms_cast_to_model")
+        if into_shard:
+            if full_flat is None or full_flat is self.data:
+                self.model_written()
+            else:
+                self.masters_written()   # model_shard now holds the cast of another buffer
 
     # ---------------------------------------------------- stage-3 params
     @torch.no_grad()
     def partition_params(self) -> None:
         """Keep only the owned master shard; parameters become flat
-        placeholders of their owned slices (flat.py:157-172)."""
+        placeholders of their owned slices (flat.py:157-172).  The
+        placeholders are views into one model-dtype buffer of the shard,
+        ``model_shard``."""
         if self._partitioned:
             return
         self.data = self.data[self.shard_start:self.shard_end].clone()
+        self.model_shard = torch.empty(self.numel_shard(), dtype=self.model_dtype(), device=self.device)
         self._partitioned = True
+        self._materialized = True      # full-shaped until dematerialized
         self.dematerialize_params()
         self.copy_flat_to_model()
 
     @torch.no_grad()
     def materialize_params(self) -> None:
-        if not self._partitioned:
+        """Give the parameters their full shapes (flat.py:174-182).  At world
+        size 1 they become views into ``model_shard``, which already holds the
+        cast of the masters whenever :meth:`model_is_fresh`; with more ranks
+        they are views into one full model-dtype buffer that the caller
+        fills (the all-gather target)."""
+        if not self._partitioned or self._materialized:
             return
-        for p, shape in zip(self.params, self._shapes):
-            p.data = torch.empty(shape, dtype=p.data.dtype, device=p.data.device)
+        if self.whole_range:
+            if self._full_views is None:
+                self._full_views = [self.model_shard[off:off + n].view(shape) for off, n, shape
+                                    in zip(self.layout.offsets, self._numels, self._shapes)]
+            views = self._full_views
+        else:
+            base = self._full_model = torch.empty(self.numel_padded, dtype=self.model_shard.dtype,
+                                                  device=self.device)
+            views = [base[off:off + n].view(shape) for off, n, shape
+                     in zip(self.layout.offsets, self._numels, self._shapes)]
+        for p, view in zip(self.params, views):
+            p.data = view
+        self._materialized = True
 
     @torch.no_grad()
     def dematerialize_params(self) -> None:
-        if not self._partitioned:
+        """Parameters drop back to flat views of their owned slices in
+        ``model_shard`` (flat.py:184-193); nothing is allocated or copied."""
+        if not self._partitioned or not self._materialized:
             return
-        for (offset, p), n in zip(self._offsets, self._numels):
-            lo, hi = _overlap((offset, offset + n), (self.shard_start, self.shard_end))
-            p.data = torch.empty(max(0, hi - lo), dtype=p.data.dtype, device=p.data.device)
+        if self._shard_views is None:
+            ms, me = self.shard_start, self.shard_end
+            self._shard_views = []
+            for off, n in zip(self.layout.offsets, self._numels):
+                lo, hi = _overlap((off, off + n), (ms, me))
+                self._shard_views.append(self.model_shard[lo - ms:hi - ms])
+        for p, view in zip(self.params, self._shard_views):
+            p.data = view
+        self._full_model = None
+        self._materialized = False
+
+    def _params_view_model_shard(self) -> bool:
+        """The parameters' storage is exactly ``model_shard`` (freed, or
+        gathered at world size 1)."""
+        return self._partitioned and (not self._materialized or self.whole_range)
+
+    def _token(self) -> Tuple[int, int, int]:
+        # in-place writes to `data` or to any parameter (placeholder or
+        # gathered view) advance these torch version counters
+        return (self.data.data_ptr(), self.data._version,
+                sum(p._version for p in self.params))
+
+    def model_is_fresh(self) -> bool:
+        """``model_shard`` holds the model-dtype cast of the current masters
+        and nothing has been written into the parameters since."""
+        return self._model_token is not None and self._model_token == self._token()
+
+    def model_written(self) -> None:
+        """Record that ``model_shard`` was just given the cast of ``data``."""
+        if self._partitioned:
+            self._model_token = self._token()
+
+    def masters_written(self) -> None:
+        """Record that ``data`` changed without the cast into ``model_shard``
+        (kernels write through raw addresses, which torch's version counter
+        does not see)."""
+        self._model_token = None
 
     # ------------------------------------------------ boundary pointers
     @property

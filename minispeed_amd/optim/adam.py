@@ -77,6 +77,7 @@ class FlatAdam:
                 ctypes.byref(hp), self._clean.data_ptr(), _native.stream_handle(flat.device),
             )
             _native.check(rc, "ms_fused_adamw")
+            flat.masters_written()
         return True
 
     def zero_grad(self) -> None:

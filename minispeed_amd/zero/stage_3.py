@@ -2,17 +2,20 @@
 
 Between steps every parameter is a flat model-dtype placeholder of its owned
 slice and the masters are the owned shard; ``gather_parameters`` gives the
-parameters their real shapes and casts the masters into them (the
+parameters their real shapes holding the cast of the masters (the
 cast-on-gather, stage_3.py:67-86), ``free_parameters`` drops them back to
 placeholders refreshed from the masters (stage_3.py:88-100).
 
-In the fused boundary the placeholders are created before K3 runs and K3
-writes the cast of the updated masters straight into them, which is what
-the reference's Adam step followed by ``free_parameters`` leaves behind.  On
-a skipped step the masters are unchanged and the placeholders are filled by
-the cast kernel instead.  At world size 1 the all-gather is the identity, so
-the gather casts from the master shard directly instead of through a
-transient full fp32 copy: the cast is elementwise, the result identical.
+The placeholders are views into one model-dtype buffer of the shard
+(``FlatParamGroup.model_shard``), and at world size 1 the gathered
+parameters are shaped views into the same buffer: the gather is a change of
+views, and the cast runs only when the buffer does not already hold the cast
+of the current masters (after a boundary taken without a gather, a
+standalone ``step()``, or an in-place write to the masters or parameters).
+In the fused boundary K3 writes the cast of the updated masters straight
+into the buffer, which is what the reference's Adam step followed by
+``free_parameters`` leaves behind.  On a skipped step the masters are
+unchanged and the buffer is refreshed by the cast kernel instead.
 """
 
 from __future__ import annotations
@@ -48,7 +51,8 @@ class ZeROStage3Optimizer(ZeROOptimizer):
                     f"(shard {g.numel_shard()} of {g.numel_padded})"
                 )
             g.materialize_params()
-            g.copy_flat_to_model(g.data)
+            if not g.model_is_fresh():
+                g.copy_flat_to_model()
         self._gathered = True
 
     @torch.no_grad()
@@ -66,7 +70,7 @@ class ZeROStage3Optimizer(ZeROOptimizer):
 
     @torch.no_grad()
     def step(self) -> bool:
-        self.adam.step()
+        self.adam.step()     # marks the groups' model copies stale
         return True
 
     # ------------------------------------------------------ fused boundary
@@ -82,11 +86,16 @@ class ZeROStage3Optimizer(ZeROOptimizer):
 
     def _after_boundary(self, overflow: bool) -> None:
         if self._boundary_freed:
-            if overflow:
-                for g in self.flat_groups:
+            for g in self.flat_groups:
+                if overflow:
                     g.copy_flat_to_model()
+                else:
+                    g.model_written()     # K3 wrote the cast of the new masters
             self._gathered = False
             self._boundary_freed = False
+        elif not overflow:
+            for g in self.flat_groups:
+                g.masters_written()       # placeholders keep the old values
         for g in self.flat_groups:
             if g.grad is not None:
                 g.grad = None  # the full flat grad never outlives the boundary
