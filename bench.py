@@ -1,7 +1,7 @@
 """Boundary-step throughput of minispeed_amd on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload gpt-1.3b | llama3-8b-shard]
-                    [--grad-dtype fp16] [--mode fused|materialize] [--zero-stage 1]
+                    [--grad-dtype fp16] [--mode fused|materialize|contiguous] [--zero-stage 1]
                     [--no-cpu-baseline] [--copy-calibration]
 
 A step is one gradient-accumulation boundary through the engine API
@@ -49,6 +49,8 @@ BYTES = {
     ("materialize", 2): (6, 30),   # K1 read g2 write f4 | K3 read f4+12, write 12+2
     ("fused", 4): (4, 32),
     ("materialize", 4): (8, 32),
+    ("contiguous", 2): (4, 30),    # K1 read fp32 sum 4 | K3 read 4+12, write 12+2
+    ("contiguous", 4): (4, 30),
 }
 
 
@@ -63,7 +65,7 @@ def parse(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gpt-1.3b")
     ap.add_argument("--grad-dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
-    ap.add_argument("--mode", default="fused", choices=["fused", "materialize"])
+    ap.add_argument("--mode", default="fused", choices=["fused", "materialize", "contiguous"])
     ap.add_argument("--zero-stage", type=int, default=1, choices=[0, 1, 2, 3],
                     help="ZeRO stage at world size 1 (3: also times the parameter gather)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -85,7 +87,8 @@ def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1) -> dict:
                       "params": {"warmup_min_lr": 0.0, "warmup_max_lr": 1e-3,
                                  "warmup_num_steps": 100, "total_num_steps": 1000}},
         "zero_optimization": {"stage": zero_stage},
-        "hip_boundary": {"materialize_flat_grad": mode == "materialize"},
+        "hip_boundary": {"materialize_flat_grad": mode == "materialize",
+                         "contiguous_gradients": mode == "contiguous"},
         "steps_per_print": 1000000,
     }
     if grad_dtype == "fp16":
@@ -339,6 +342,7 @@ def main(argv=None) -> int:
     log("[bench] buffers resident; warming up")
 
     gather_s = []
+    accum_s = []
 
     def attach(k: int) -> None:
         """What the last backward of a window leaves: grads on every param
@@ -351,6 +355,15 @@ def main(argv=None) -> int:
             gather_s.append(time.perf_counter() - t0)
         for p, g in zip(params, grad_sets[k % 2]):
             p.grad = g
+        if engine.contiguous is not None:
+            # what the post-accumulate-grad hooks do during the backward of a
+            # one-micro-batch window, timed on its own
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i, p in enumerate(params):
+                engine.contiguous.accumulate(0, i, p)
+            torch.cuda.synchronize()
+            accum_s.append(time.perf_counter() - t0)
         engine.micro_steps += 1
 
     def boundary() -> None:
@@ -362,6 +375,7 @@ def main(argv=None) -> int:
         boundary()
     torch.cuda.synchronize()
     gather_s.clear()
+    accum_s.clear()
     timer = LaunchTimer()
     engine.optimizer.launch_timer = timer
     step_s = []
@@ -438,6 +452,8 @@ def main(argv=None) -> int:
         },
         "cpu_baseline": None,
     }
+    if accum_s:
+        result["contiguous"] = {"accumulate_ms_per_micro_batch": round(float(np.mean(accum_s)) * 1e3, 4)}
     if args.zero_stage == 3:
         # the gather is a change of views; a stale copy would cost one cast
         engine.optimizer.gather_parameters()

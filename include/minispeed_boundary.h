@@ -200,6 +200,18 @@ int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
                      const ms_segment_t* segs, int32_t nseg,
                      int32_t model_dtype, void* stream);
 
+/*
+ * K5 — opt-in contiguous gradients: dst[i] = (first ? 0 : dst[i]) +
+ * (float)src[i] for i in [0, n), dst [dev] fp32, src [dev] of src_dtype.
+ * Called once per parameter per micro-batch (a post-accumulate-grad hook),
+ * it replaces autograd's accumulation into param.grad across the
+ * micro-batches of a window (engine.py:235-251) followed by flatten_grads
+ * (flat.py:196-213), accumulating in fp32 instead of the parameter dtype.
+ * Not bitwise the reference by design: minispeed has no such mode.
+ */
+int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n,
+                       int32_t first, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -110,6 +110,7 @@ SIGNATURES = {
          ctypes.POINTER(AdamWParams), _P, _P],
     ),
     "ms_cast_to_model": (ctypes.c_int, [_P, _I64, _I64, _P, _I32, _I32, _P]),
+    "ms_accumulate_grad": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _P]),
 }
 
 _lock = threading.Lock()

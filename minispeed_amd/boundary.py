@@ -163,7 +163,8 @@ class GroupLaunch:
     step: int                     # Adam step number this update would use
     exp_avg: torch.Tensor         # owned-range moments (optim/adam.py:58-65)
     exp_avg_sq: torch.Tensor
-    grads: List[int]              # gradient address per parameter (0: none)
+    grads: Sequence[int]          # gradient address per parameter (0: none)
+    grad_dtype: Optional[int] = None   # MS_DTYPE_* of the gradients (default: the params')
 
 
 def run_boundary(
@@ -200,6 +201,7 @@ def run_boundary(
     for gi, gl in enumerate(launches):
         g = gl.group
         dtype = _native.ms_dtype(g.params[0].dtype)
+        gdtype = dtype if gl.grad_dtype is None else gl.grad_dtype
         flat_out = None
         if materialize_flat_grad:
             if g.grad is None:
@@ -211,13 +213,13 @@ def run_boundary(
         psum, pflag = ws.partial_ptrs(gi)
         tok = timer.start("k1")
         rc = lib.ms_grad_stats(
-            t1[0], t1[1], dtype, 0, g.numel_padded, lo, hi, 1 if unscale else 0, scale32,
+            t1[0], t1[1], gdtype, 0, g.numel_padded, lo, hi, 1 if unscale else 0, scale32,
             flat_out.data_ptr() if flat_out is not None else None,
             psum, pflag, ws.nblk, stream,
         )
         timer.stop(tok)
         _native.check(rc, "ms_grad_stats")
-        dtypes.append(dtype)
+        dtypes.append((gdtype, dtype))
         flats.append(flat_out)
 
     tok = timer.start("k2")
@@ -234,7 +236,7 @@ def run_boundary(
     ws.start_readback()
 
     models = model_targets()
-    for gl, dtype, flat_out, mptrs in zip(launches, dtypes, flats, models):
+    for gl, (gdtype, dtype), flat_out, mptrs in zip(launches, dtypes, flats, models):
         g = gl.group
         lo, hi = g.own_range
         if hi <= lo:
@@ -252,7 +254,7 @@ def run_boundary(
         tok = timer.start("k3")
         rc = lib.ms_fused_adamw(
             master.data_ptr(), gl.exp_avg.data_ptr(), gl.exp_avg_sq.data_ptr(), fg_ptr,
-            t3[0], t3[1], dtype, dtype, lo, hi, ctypes.byref(hp), ws.scalars.data_ptr(), stream,
+            t3[0], t3[1], gdtype, dtype, lo, hi, ctypes.byref(hp), ws.scalars.data_ptr(), stream,
         )
         timer.stop(tok)
         _native.check(rc, "ms_fused_adamw")

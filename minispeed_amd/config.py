@@ -13,14 +13,20 @@ minispeed config drives this package unchanged:
     scheduler.{type, params}                           (config.py:142-155)
     steps_per_print, seed, drop_overflow_on_loss       (config.py:158-160)
 
-One key is specific to this package and ignored by minispeed:
+One section is specific to this package and ignored by minispeed:
 
-    "hip_boundary": {"materialize_flat_grad": false}
+    "hip_boundary": {"materialize_flat_grad": false, "contiguous_gradients": false}
 
 With ``materialize_flat_grad`` the ragged-grad kernel also writes the fp32
 flat gradient buffer and the AdamW kernel reads it back (36 B/param for half
 grads); by default the AdamW kernel re-reads the ragged half gradients and
 the flat buffer is never written (30 B/param).  Both give identical results.
+
+``contiguous_gradients`` (opt-in) accumulates every micro-batch gradient in
+fp32 straight into a flat buffer as backward produces it, instead of in the
+parameter dtype in ``param.grad``; ``param.grad`` is released after each
+backward.  This changes the numerics (fp32 instead of half accumulation), so
+it is not bitwise minispeed and is off by default.
 """
 
 from __future__ import annotations
@@ -76,6 +82,7 @@ class DeepSpeedConfig:
         self.drop_overflow = bool(raw.get("drop_overflow_on_loss", True))
         hip = _section(raw, "hip_boundary")
         self.materialize_flat_grad = bool(hip.get("materialize_flat_grad", False))
+        self.contiguous_gradients = bool(hip.get("contiguous_gradients", False))
 
     # ------------------------------------------------------------ sections
     def _parse_batch(self, raw: dict, world: int) -> None:

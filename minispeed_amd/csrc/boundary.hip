@@ -12,6 +12,8 @@
 //                     owned range              (optim/adam.py:59-93,
 //                                                flat.py:133-154)
 //   K4 k_cast         fp32 master -> model dtype (ZeRO-3 gather/free)
+//   K5 k_accumulate   opt-in fp32 accumulation of one micro-batch gradient
+//                     into its flat slice (contiguous gradients)
 //
 // Everything here is HBM-bound streaming; no MFMA.  Work is cut into tiles
 // of kTile consecutive flat indices; a lane owns kVec consecutive elements
@@ -616,6 +618,42 @@ __global__ __launch_bounds__(kThreads) void k_cast(
   }
 }
 
+// ------------------------------------------------------------------ K5
+// dst[i] = (first ? 0 : dst[i]) + widen(src[i]) over one parameter's flat
+// slice, i in [0, n): one fp32 rounding per add, as torch's fp32 add_ of a
+// widened tensor.  The vector path needs both addresses 16-byte aligned;
+// otherwise every lane steps element by element.
+template <class D>
+__global__ __launch_bounds__(kThreads) void k_accumulate(
+    float* __restrict__ dst, const void* __restrict__ src, int64_t n, int first) {
+  const bool vec = aligned16(dst) && aligned16(src);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  int64_t done = 0;
+  if (vec) {
+    const int64_t nvec = n / kVec;
+    for (int64_t c = tid; c < nvec; c += stride) {
+      typename D::raw r[kVec];
+      load_raw8<D>(static_cast<const char*>(src) + c * kVec * D::kBytes, r);
+      float x[kVec];
+      if (first) {
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) x[k] = D::widen(r[k]);
+      } else {
+        load_f8(dst + c * kVec, x);
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) x[k] = x[k] + D::widen(r[k]);
+      }
+      store_f8(dst + c * kVec, x);
+    }
+    done = nvec * kVec;
+  }
+  for (int64_t i = done + tid; i < n; i += stride) {
+    const float g = D::widen(load_raw1<D>(src, i));
+    dst[i] = first ? g : dst[i] + g;
+  }
+}
+
 // ------------------------------------------------------------- launching
 int cu_count() {
   static int cached = 0;
@@ -842,6 +880,29 @@ int ms_fused_adamw(float* master, float* exp_avg, float* exp_avg_sq,
     default:
       launch_adamw_m<DBF16>(model_dtype, master, exp_avg, exp_avg_sq, flat_grad,
                             segs, nseg, begin, end, h, scalars, st);
+      break;
+  }
+  return launch_status();
+}
+
+int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n,
+                       int32_t first, void* stream) {
+  if (!valid_dtype(src_dtype) || n < 0) return MS_EINVAL;
+  if (n == 0) return MS_OK;
+  if (!dst || !src) return MS_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(stream_grid((n + kTile - 1) / kTile, 0));
+  const dim3 block(kThreads);
+  const int f = first ? 1 : 0;
+  switch (src_dtype) {
+    case MS_DTYPE_F32:
+      hipLaunchKernelGGL(k_accumulate<DF32>, grid, block, 0, st, dst, src, n, f);
+      break;
+    case MS_DTYPE_F16:
+      hipLaunchKernelGGL(k_accumulate<DF16>, grid, block, 0, st, dst, src, n, f);
+      break;
+    default:
+      hipLaunchKernelGGL(k_accumulate<DBF16>, grid, block, 0, st, dst, src, n, f);
       break;
   }
   return launch_status();

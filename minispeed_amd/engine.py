@@ -29,6 +29,7 @@ from torch import nn
 from . import _native, comm
 from . import checkpoint as ckpt
 from .config import DeepSpeedConfig, load_config
+from .contiguous import ContiguousGradients
 from .flat import FlatParamGroup, build_flat_groups
 from .optim import build_scheduler
 from .precision import DynamicLossScaler
@@ -103,6 +104,10 @@ class DeepSpeedEngine:
                 g.partition_params()
 
         self.optimizer = build_zero_optimizer(self.flat_groups, option_groups, zero_stage=self.config.zero_stage)
+        self.contiguous: Optional[ContiguousGradients] = None
+        if self.config.contiguous_gradients:
+            self.contiguous = ContiguousGradients(self.flat_groups)
+            self.optimizer.contiguous = self.contiguous
         self.lr_scheduler = build_scheduler(
             self.optimizer, self.config.scheduler_type, self.config.scheduler_params
         )
@@ -211,6 +216,8 @@ class DeepSpeedEngine:
             materialize_flat_grad=self.config.materialize_flat_grad,
         )
         self.last_boundary = scalars
+        if self.contiguous is not None:
+            self.contiguous.next_window()
         overflow = bool(scalars.overflow)
         self.loss_scaler.update(overflow=overflow)
         self._check_device_scaler(scalars)
@@ -244,6 +251,8 @@ class DeepSpeedEngine:
             )
 
     def zero_grad(self, set_to_none: bool = True) -> None:
+        if self.contiguous is not None:
+            self.contiguous.next_window()
         for g in self.flat_groups:
             g.zero_grad()
         for p in self.module.parameters():

@@ -16,7 +16,7 @@ from typing import List, Optional
 
 import torch
 
-from .. import comm
+from .. import _native, comm
 from ..boundary import GroupLaunch, LaunchTimer, Workspace, run_boundary
 from ..flat import FlatParamGroup
 from ..optim.adam import FlatAdam
@@ -34,6 +34,8 @@ class ZeROOptimizer:
         self.grad_norm: Optional[float] = None
         self._workspace: Optional[Workspace] = None
         self.launch_timer: Optional[LaunchTimer] = None  # HIP-event timing hook
+        # opt-in fp32 gradient accumulation (contiguous.py); set by the engine
+        self.contiguous = None
 
     # ------------------------------------------------------ torch-ish surface
     @property
@@ -99,14 +101,19 @@ class ZeROOptimizer:
         ws = self._ws()
         keep: List[torch.Tensor] = []
         launches = []
-        for g, group, state in zip(self.flat_groups, self.adam.param_groups, self.adam.state):
-            ptrs, tensors = g.grad_pointers()
-            keep.extend(tensors)
+        for gi, (g, group, state) in enumerate(zip(self.flat_groups, self.adam.param_groups,
+                                                   self.adam.state)):
+            grad_dtype = None
+            if self.contiguous is not None:
+                ptrs, grad_dtype = self.contiguous.grad_pointers(gi), _native.DTYPE_F32
+            else:
+                ptrs, tensors = g.grad_pointers()
+                keep.extend(tensors)
             lr, betas, eps, wd = FlatAdam.hyper(group)
             launches.append(GroupLaunch(
                 group=g, lr=lr, betas=betas, eps=eps, weight_decay=wd,
                 step=state["step"] + 1, exp_avg=state["exp_avg"], exp_avg_sq=state["exp_avg_sq"],
-                grads=ptrs,
+                grads=ptrs, grad_dtype=grad_dtype,
             ))
 
         def model_targets():

@@ -377,9 +377,19 @@ class Engine:
                 g.copy_flat_to_model()
 
     @torch.no_grad()
-    def take_step(self) -> bool:                                          # engine.py:268-322
-        for g in self.groups:
-            g.flatten_grads()
+    def take_step(self, flat_grads=None) -> bool:                         # engine.py:268-322
+        """``flat_grads`` (one fp32 flat tensor per group, numel_padded)
+        stands in for the flatten of ``param.grad``: the boundary of the
+        opt-in contiguous-gradient mode, which minispeed does not have; every
+        later step is the reference's."""
+        if flat_grads is None:
+            for g in self.groups:
+                g.flatten_grads()
+        else:
+            for g, f in zip(self.groups, flat_grads):
+                g.grad = f.to(torch.float32).clone()
+                for p in g.params:
+                    p.grad = None
         overflow = any(has_overflow(g.grad) for g in self.groups)
         if overflow:
             self.scaler.update(overflow=True)
@@ -426,10 +436,17 @@ class Engine:
             if not g.partitioned:
                 g.copy_flat_to_model()
 
-    def step(self) -> bool:                                               # engine.py:254-266
+    def step(self, flat_grads=None) -> bool:                              # engine.py:254-266
         if not (self.micro_steps > 0 and self.micro_steps % self.gas == 0):
             return False
         if getattr(self, "_consumed", -1) == self.micro_steps:
             return False
         self._consumed = self.micro_steps
-        return self.take_step()
+        return self.take_step(flat_grads)
+
+
+def accumulate_fp32(acc: Optional[torch.Tensor], grad: torch.Tensor) -> torch.Tensor:
+    """One micro-batch of the opt-in contiguous-gradient mode: the gradient
+    widened to fp32 and added to the running fp32 sum (one rounding)."""
+    g = grad.detach().reshape(-1).to(torch.float32)
+    return g.clone() if acc is None else acc + g

@@ -1,0 +1,212 @@
+"""Opt-in contiguous gradients on the GPU.
+
+* K5 (``ms_accumulate_grad``) against the fp32 sum of widened gradients,
+  bit for bit, for every dtype, aligned and misaligned slices, ragged sizes,
+  inf/nan;
+* the engine in this mode against the oracle's boundary given the fp32 sums
+  (bit-exact flags, scale and Adam moments when the clip coefficients agree;
+  masters within 2 fp32 ulp per step; norm within 1e-5), through real
+  backward passes with gradient accumulation;
+* where half-precision accumulation is exact the mode equals the default
+  mode bit for bit; parameters without a gradient in a window count as
+  zeros; an overflow skips the step and the next window starts clean;
+  ZeRO-3 equals ZeRO-0.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import minispeed_amd as ms
+from minispeed_amd import _native
+from oracle import boundary as ob
+from oracle import recipe
+from tests.helpers import master_step_within_ulps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SHAPES = [(7, 5), (3,), (16, 33), (1,), (129,), (64, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,off", [(1, 0), (7, 3), (8, 4), (2049, 1), (100003, 8), (65536, 0)])
+def test_accumulate_kernel_is_the_fp32_sum(dtype, n, off):
+    lib = _native.load()
+    g = torch.Generator(device=DEV).manual_seed(n + off)
+    parts = [torch.randn(n, generator=g, device=DEV).to(dtype) for _ in range(3)]
+    if n > 10:
+        parts[1][5] = float("inf")
+        parts[2][9] = float("nan")
+    buf = torch.full((n + off + 8,), -3.0, device=DEV)
+    dst = buf.data_ptr() + off * 4
+    stream = _native.stream_handle(torch.device(DEV))
+    want = None
+    for k, x in enumerate(parts):
+        _native.check(lib.ms_accumulate_grad(dst, x.data_ptr(), _native.ms_dtype(dtype), n,
+                                             1 if k == 0 else 0, stream), "ms_accumulate_grad")
+        want = ob.accumulate_fp32(want, x.cpu())
+        got = buf[off:off + n].cpu()
+        assert torch.equal(got.view(torch.int32)[~torch.isnan(want)],
+                           want.view(torch.int32)[~torch.isnan(want)]), k
+        assert torch.equal(torch.isnan(got), torch.isnan(want))
+    # the guard elements around the slice are untouched
+    assert torch.all(buf[:off].cpu() == -3.0) and torch.all(buf[off + n:].cpu() == -3.0)
+
+
+def test_accumulate_kernel_rejects_bad_arguments():
+    lib = _native.load()
+    x = torch.zeros(4, device=DEV)
+    assert lib.ms_accumulate_grad(None, x.data_ptr(), 0, 4, 1, None) == -1
+    assert lib.ms_accumulate_grad(x.data_ptr(), x.data_ptr(), 7, 4, 1, None) == -1
+    assert lib.ms_accumulate_grad(x.data_ptr(), x.data_ptr(), 0, -1, 1, None) == -1
+    assert lib.ms_accumulate_grad(x.data_ptr(), x.data_ptr(), 0, 0, 1, None) == 0
+
+
+class Linear(nn.Module):
+    """loss = sum_k sum(p_k * c_k): d loss / d p_k = c_k exactly."""
+
+    def __init__(self, dtype):
+        super().__init__()
+        g = torch.Generator().manual_seed(3)
+        self.ps = nn.ParameterList(nn.Parameter((torch.randn(*s, generator=g) * 0.05).to(dtype))
+                                   for s in SHAPES)
+
+    def forward(self, cs, skip=()):
+        return sum((p.float() * c).sum() for k, (p, c) in enumerate(zip(self.ps, cs))
+                   if k not in skip)
+
+
+def _cfg(dtype, stage=0, contiguous=True, gas=2):
+    cfg = {"train_micro_batch_size_per_gpu": 1, "gradient_accumulation_steps": gas,
+           "gradient_clipping": 1.0, "dtype": dtype,
+           "optimizer": {"type": "AdamW", "params": {"lr": 1e-2, "weight_decay": 0.01}},
+           "zero_optimization": {"stage": stage},
+           "hip_boundary": {"contiguous_gradients": contiguous}}
+    if dtype == "fp16":
+        cfg["fp16"] = {"enabled": True, "loss_scale": 0, "initial_scale_power": 8,
+                       "loss_scale_window": 1000}
+    return cfg
+
+
+def _coeffs(seed, dyadic):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for s in SHAPES:
+        c = torch.randn(*s, generator=g)
+        if dyadic:
+            c = torch.round(c * 16) / 16          # few significant bits: exact in half
+        out.append(c.to(DEV))
+    return out
+
+
+def _run(dtype, stage, contiguous, windows, dyadic, skip_at=None, inf_at=None, gas=2):
+    torch.manual_seed(0)
+    model = Linear({"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dtype]).to(DEV)
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=_cfg(dtype, stage, contiguous, gas))
+    applied = []
+    for w in range(windows):
+        for m in range(gas):
+            skip = (2,) if skip_at == w else ()
+            loss = engine(_coeffs(100 * w + m, dyadic), skip)
+            engine.backward(loss)
+            if contiguous:
+                assert all(p.grad is None for p in model.parameters())
+            if inf_at == (w, m):
+                if contiguous:
+                    engine.contiguous.accum[0][10] = float("inf")
+                else:
+                    next(iter(model.parameters())).grad.view(-1)[0] = float("inf")
+            applied.append(engine.step())
+    return engine, model, applied
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_equals_default_mode_where_half_accumulation_is_exact(dtype):
+    a, ma, ra = _run(dtype, 0, False, 4, dyadic=True)
+    b, mb, rb = _run(dtype, 0, True, 4, dyadic=True)
+    assert ra == rb
+    assert a.grad_norm == b.grad_norm and a.get_loss_scale() == b.get_loss_scale()
+    assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
+    assert torch.equal(a.optimizer.state[0]["exp_avg_sq"], b.optimizer.state[0]["exp_avg_sq"])
+
+
+def test_missing_gradients_count_as_zero_and_do_not_leak_from_earlier_windows():
+    a, _, _ = _run("bf16", 0, False, 3, dyadic=True, skip_at=1)
+    b, _, _ = _run("bf16", 0, True, 3, dyadic=True, skip_at=1)
+    assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
+    assert a.grad_norm == b.grad_norm
+
+
+def test_overflow_skips_and_the_next_window_starts_clean():
+    a, _, ra = _run("fp16", 0, False, 3, dyadic=True, inf_at=(1, 1))
+    b, _, rb = _run("fp16", 0, True, 3, dyadic=True, inf_at=(1, 1))
+    assert ra == rb and rb.count(True) == 2 and b.skipped_steps == 1
+    assert a.get_loss_scale() == b.get_loss_scale() == 2.0 ** 7
+    assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
+
+
+def test_stage3_equals_stage0():
+    a, _, _ = _run("fp16", 0, True, 3, dyadic=False)
+    b, _, _ = _run("fp16", 3, True, 3, dyadic=False)
+    assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
+    assert a.grad_norm == b.grad_norm
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_matches_the_oracle_given_the_fp32_sums(dtype):
+    """Non-dyadic gradients: fp32 sums differ from half sums; each boundary
+    is checked against the oracle started from the GPU's state."""
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16}[dtype]
+    torch.manual_seed(0)
+    model = Linear(tdt).to(DEV)
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=_cfg(dtype, 0, True, gas=3))
+    ref_params = [nn.Parameter(p.detach().cpu().clone()) for p in model.parameters()]
+    ref = ob.Engine([ref_params], [{"lr": 1e-2, "betas": (0.9, 0.999), "eps": 1e-8,
+                                    "weight_decay": 0.01}], dtype=dtype, zero_stage=0, clip=1.0,
+                    initial_scale_power=8, loss_scale_window=1000)
+    g = engine.flat_groups[0]
+    differs = False
+    for w in range(4):
+        sums = [None] * len(SHAPES)
+        for m in range(3):
+            cs = _coeffs(10 * w + m, dyadic=False)
+            loss = engine(cs)
+            engine.backward(loss)
+            factor = engine.loss_scaler.loss_scale_factor / 3
+            # the gradient autograd hands the hook: the engine casts the
+            # floating inputs to the parameter dtype, the product rounds in
+            # fp32, and the backward of p.float() rounds to the parameter dtype
+            for k, c in enumerate(cs):
+                c_in = c.cpu().to(tdt).float()
+                sums[k] = ob.accumulate_fp32(sums[k], (c_in * np.float32(factor)).to(tdt))
+        flat = torch.zeros(g.numel_padded)
+        for off, s in zip(g.layout.offsets, sums):
+            flat[off:off + s.numel()] = s
+        before = g.data.detach().cpu()
+        st = engine.optimizer.state[0]
+        ref.load_state([before], [st["exp_avg"].cpu()], [st["exp_avg_sq"].cpu()], [st["step"]],
+                       (engine.loss_scaler.scale, engine.loss_scaler.good_steps,
+                        engine.loss_scaler.skipped_steps),
+                       engine.lr_scheduler.last_epoch,
+                       [pg["lr"] for pg in engine.optimizer.param_groups])
+        ref.micro_steps += 3
+        assert engine.step() is True and ref.step(flat_grads=[flat]) is True
+        assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
+        _, _, coef = recipe.clip_coef(np.float32(ref.grad_norm), 1.0)
+        same = np.float32(engine.last_boundary.coef) == np.float32(coef)
+        ok, worst = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
+                                            ref.groups[0].data.numpy(), 2.0 if same else 4.0)
+        assert ok, (w, worst)
+        if same:
+            assert torch.equal(st["exp_avg"].cpu(), ref.state[0]["exp_avg"])
+            assert torch.equal(st["exp_avg_sq"].cpu(), ref.state[0]["exp_avg_sq"])
+        # the fp32 sums are not half values: half accumulation would differ
+        differs = differs or not torch.equal(sums[2].to(tdt).float(), sums[2])
+    assert differs
