@@ -69,7 +69,8 @@ def parse(argv=None):
     ap.add_argument("--zero-stage", type=int, default=1, choices=[0, 1, 2, 3],
                     help="ZeRO stage at world size 1 (3: also times the parameter gather)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-params", type=int, default=50_000_000)
+    ap.add_argument("--cpu-sample-params", type=int, default=0,
+                    help="CPU baseline sample (0: the whole workload, ~1 minute at 1.3B)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (a counter yardstick for rocprofv3 --pmc)")
     return ap.parse_args(argv)
@@ -97,9 +98,21 @@ def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1) -> dict:
     return cfg
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo", "r", encoding="utf-8") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
     """Time the oracle's torch restatement of the reference boundary step on
-    the host cores over the leading tensors of the same list."""
+    the host cores: the whole tensor list (``sample_params <= 0``) or its
+    leading transformer layers up to ``sample_params``."""
     import torch
     from torch import nn
 
@@ -108,10 +121,11 @@ def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     threads = max(1, min(threads, 16))
     torch.set_num_threads(threads)
-    # whole transformer layers after the embeddings, until the sample size
+    # the whole list, or whole transformer layers after the embeddings until
+    # the sample size
     sample, total = [], 0
-    for s in shapes[2:]:
-        if total >= sample_params:
+    for s in (shapes if sample_params <= 0 else shapes[2:]):
+        if 0 < sample_params <= total:
             break
         n = 1
         for x in s:
@@ -138,15 +152,18 @@ def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
         assert ok
     times = sorted(times[1:])
     med = times[len(times) // 2]
+    what = ("the whole workload" if len(sample) == len(shapes)
+            else "the leading transformer layers of the same list")
     return {
         "value": total / med / 1e9,
         "unit": "Gparams/s",
         "cores": threads,
         "kind": "port",
         "sample": (f"oracle torch-CPU restatement of the reference step on {len(sample)} tensors "
-                   f"({total:,} params: the leading transformer layers of the same list); "
-                   f"median of 3 steps after 1 warm-up, "
-                   f"{med * 1e3:.0f} ms/step"),
+                   f"({total:,} params: {what}); median of 3 steps after 1 warm-up, "
+                   f"{med * 1e3:.0f} ms/step; {threads} threads of {os.cpu_count()} on "
+                   f"{cpu_model()}"),
+        "gbps_at_30_bytes": round(30 * total / med / 1e9, 2),
     }
 
 
@@ -418,6 +435,7 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(float(np.median(step_s)) * 1e3, 4),
         "ms_per_step_with_grad_attach": round(loop_s / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
