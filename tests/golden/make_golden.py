@@ -14,7 +14,11 @@ between boundaries (the engine's micro-step counter is advanced as
 
 Two engine-level traces (an MLP trained through autograd, fp32 and bf16,
 gas 2) record losses and parameters; they pin the host-side loss scaling and
-boundary gating as well.
+boundary gating as well.  A third runs the tiny decoder LM of
+``tests/tinylm.py`` (3.3M parameters, fp32, ZeRO 0, 20 steps) and records
+its losses, gradient norms and per-tensor parameter sums (``cases.json`` key
+``tinylm``): an end-to-end trace through autograd, compared on the GPU at a
+tolerance that allows for CPU/GPU floating-point differences.
 
 Three cases also write a checkpoint with minispeed's own
 ``engine.save_checkpoint`` part-way through (``CHECKPOINTS``: case -> number
@@ -41,6 +45,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
 
 SHAPES = [(7, 5), (3,), (16, 33), (1,), (129,)]
 
@@ -227,6 +232,32 @@ def run_mlp_trace(ms, name, dtype, out_arrays, meta, steps=4, gas=2, micro=4):
                   "global_steps": engine.global_steps}
 
 
+def run_tinylm_trace(ms, meta, steps=20):
+    import copy
+
+    if REPO not in sys.path:
+        sys.path.insert(0, REPO)
+    from tests import tinylm
+
+    model = tinylm.build(0)
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=copy.deepcopy(tinylm.CONFIG))
+    data = tinylm.batches(steps, seed=1)
+    losses, norms = [], []
+    for s in range(steps):
+        idx = data[s]
+        loss = tinylm.loss_fn(engine(idx[:, :-1]), idx)
+        losses.append(float(loss.detach()))
+        engine.backward(loss)
+        assert engine.step()
+        norms.append(float(engine.grad_norm))
+    sums = {name: [float(p.detach().double().sum()), float(p.detach().double().pow(2).sum())]
+            for name, p in model.named_parameters()}
+    meta["tinylm"] = {"config": tinylm.CONFIG, "steps": steps, "init_seed": 0, "data_seed": 1,
+                      "losses": losses, "grad_norms": norms, "global_steps": engine.global_steps,
+                      "param_sum_sumsq": sums}
+
+
 def save_npz(name, arrays):
     """Write ``<name>.npz`` unless it already holds exactly these arrays
     (the zip container stamps times, so rewriting would churn the file)."""
@@ -262,6 +293,7 @@ def main(argv=None):
         arrays = {}
         run_mlp_trace(ms, name, dtype, arrays, meta["cases"])
         save_npz(name, arrays)
+    run_tinylm_trace(ms, meta)
     with open(os.path.join(HERE, "cases.json"), "w", encoding="utf-8") as fh:
         json.dump(meta, fh, indent=1, sort_keys=True)
     print("wrote", sorted(meta["cases"]))
