@@ -117,8 +117,10 @@ int ms_abi_version(void);
 /* Static text for a return code of this library. */
 const char* ms_error_string(int code);
 
-/* Fixed number of per-group partial slots K1 writes; a constant, so the
- * two-level norm reduction is run-to-run deterministic. */
+/* Number of per-group partial slots K1 fills (a constant).  K1 runs
+ * min(ms_stats_blocks(), ceil(n / 32768)) blocks over n flat indices, a pure
+ * function of n, and zero-fills the remaining slots, so the two-level norm
+ * reduction is run-to-run deterministic. */
 int ms_stats_blocks(void);
 
 /*
@@ -135,7 +137,8 @@ int ms_stats_blocks(void);
  *   - flat_grad [dev, optional]: flat_grad[i - begin] = g for every i;
  *   - block_sumsq [dev, optional]: per-block fp64 sum of g*g over the owned
  *     range [own_begin, own_end); with block_flag [dev] it must hold
- *     nblk >= ms_stats_blocks() slots, and every slot is written.
+ *     nblk >= ms_stats_blocks() slots, and all nblk slots are written
+ *     (zeros after the last block's).
  * With block_sumsq == NULL and block_flag == NULL the call is a pure ragged
  * flatten (FlatParamGroup.copy_model_to_flat, flat.py:115-131).
  */

@@ -43,7 +43,15 @@ namespace {
 constexpr int kThreads = 128;
 constexpr int kVec = 8;                   // elements per lane per tile
 constexpr int kTile = kThreads * kVec;    // 1024 flat elements
-constexpr int kStatsBlocks = 16384;       // fixed K1 grid (determinism)
+constexpr int kStatsBlocks = 16384;       // K1 partial slots per group
+#ifndef MS_STATS_MIN_CHUNK
+#define MS_STATS_MIN_CHUNK 32768
+#endif
+// K1 gives each block at least this many flat indices: a group of n
+// elements uses min(kStatsBlocks, ceil(n / kStatsMinChunk)) blocks, a pure
+// function of n, so the partition (and the norm's bits) never varies run
+// to run, and small groups do not pay for 16384 mostly idle blocks.
+constexpr int64_t kStatsMinChunk = MS_STATS_MIN_CHUNK;
 constexpr int kScanThreads = 512;         // K1 block: 8 wave64
 constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
 constexpr int kMaxSegs = 1 << 26;
@@ -240,7 +248,7 @@ __device__ inline double wave_sum(double x) {
 }
 
 // ------------------------------------------------------------------ K1
-// Block b of the fixed grid (kStatsBlocks blocks) owns the contiguous flat
+// Block b of the grid (stats_grid(n) blocks) owns the contiguous flat
 // range [begin + b*chunk, begin + (b+1)*chunk), chunk a multiple of kVec,
 // and walks the segments inside it with a cursor.  Each piece of a segment
 // is a scalar head, a vector body of kVec-element groups (lane j of the
@@ -328,7 +336,7 @@ __global__ __launch_bounds__(kScanThreads) void k_grad_stats(
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
     int64_t end, int64_t own_begin, int64_t own_end, int umode,
     float grad_scale, float inv_scale, float* __restrict__ flat,
-    double* __restrict__ bsum, uint32_t* __restrict__ bflag) {
+    double* __restrict__ bsum, uint32_t* __restrict__ bflag, int nslots) {
   const int lane = threadIdx.x;
   GradScan<G, kFlat, kStats> sc;
   sc.umode = umode;
@@ -380,6 +388,12 @@ __global__ __launch_bounds__(kScanThreads) void k_grad_stats(
       }
       bsum[blockIdx.x] = total;
       bflag[blockIdx.x] = flag;
+    }
+    // the slots after the last block read as "nothing here" in K2
+    for (int64_t t = static_cast<int64_t>(gridDim.x) + static_cast<int64_t>(blockIdx.x) * kScanThreads + lane;
+         t < nslots; t += static_cast<int64_t>(gridDim.x) * kScanThreads) {
+      bsum[t] = 0.0;
+      bflag[t] = 0u;
     }
   }
 }
@@ -711,29 +725,37 @@ bool valid_dtype(int32_t d) {
   return d == MS_DTYPE_F32 || d == MS_DTYPE_F16 || d == MS_DTYPE_BF16;
 }
 
+// K1's block count for n flat indices (see kStatsMinChunk)
+int stats_grid(int64_t n) {
+  int64_t g = (n + kStatsMinChunk - 1) / kStatsMinChunk;
+  if (g > kStatsBlocks) g = kStatsBlocks;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
 template <class G>
 void launch_stats(const ms_segment_t* segs, int nseg, int64_t begin,
                   int64_t end, int64_t ob, int64_t oe, int unscale, float scale,
-                  float* flat, double* bsum, uint32_t* bflag, hipStream_t st) {
+                  float* flat, double* bsum, uint32_t* bflag, int nslots,
+                  hipStream_t st) {
   const bool stats = bsum != nullptr;
   float inv = 1.0f;
   const int umode = unscale_mode(unscale, scale, &inv);
   const dim3 block(kScanThreads);
+  const dim3 grid(stats_grid(end - begin));
   if (stats) {
-    const dim3 grid(kStatsBlocks);
     if (flat)
       hipLaunchKernelGGL((k_grad_stats<G, true, true>), grid, block, 0, st, segs,
                          nseg, begin, end, ob, oe, umode, scale, inv, flat,
-                         bsum, bflag);
+                         bsum, bflag, nslots);
     else
       hipLaunchKernelGGL((k_grad_stats<G, false, true>), grid, block, 0, st,
                          segs, nseg, begin, end, ob, oe, umode, scale, inv,
-                         flat, bsum, bflag);
+                         flat, bsum, bflag, nslots);
   } else {
-    const dim3 grid(kStatsBlocks);
     hipLaunchKernelGGL((k_grad_stats<G, true, false>), grid, block, 0, st, segs,
                        nseg, begin, end, ob, oe, umode, scale, inv, flat,
-                       bsum, bflag);
+                       bsum, bflag, 0);
   }
 }
 
@@ -814,15 +836,15 @@ int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
   switch (grad_dtype) {
     case MS_DTYPE_F32:
       launch_stats<DF32>(segs, nseg, begin, end, own_begin, own_end, unscale,
-                         grad_scale, flat_grad, block_sumsq, block_flag, st);
+                         grad_scale, flat_grad, block_sumsq, block_flag, nblk, st);
       break;
     case MS_DTYPE_F16:
       launch_stats<DF16>(segs, nseg, begin, end, own_begin, own_end, unscale,
-                         grad_scale, flat_grad, block_sumsq, block_flag, st);
+                         grad_scale, flat_grad, block_sumsq, block_flag, nblk, st);
       break;
     default:
       launch_stats<DBF16>(segs, nseg, begin, end, own_begin, own_end, unscale,
-                          grad_scale, flat_grad, block_sumsq, block_flag, st);
+                          grad_scale, flat_grad, block_sumsq, block_flag, nblk, st);
       break;
   }
   return launch_status();
