@@ -116,20 +116,29 @@ class LaunchTimer:
     When attached to an optimizer (``optimizer.launch_timer``), every K1 /
     K2 / K3 launch is bracketed by events recorded on the current stream,
     the stream the kernels run on.  ``durations_ms(name)`` is valid after
-    the stream has been synchronised.
+    the stream has been synchronised.  ``reserve(n)`` creates n events up
+    front, so that a timed region pays only for recording them.
     """
 
-    def __init__(self):
+    def __init__(self, reserve: int = 0):
         self._events = {}
+        self._pool: List[torch.cuda.Event] = []
+        self.reserve(reserve)
+
+    def reserve(self, n: int) -> None:
+        self._pool.extend(torch.cuda.Event(enable_timing=True) for _ in range(n))
+
+    def _event(self) -> torch.cuda.Event:
+        return self._pool.pop() if self._pool else torch.cuda.Event(enable_timing=True)
 
     def start(self, name: str):
-        ev = torch.cuda.Event(enable_timing=True)
+        ev = self._event()
         ev.record()
         return (name, ev)
 
     def stop(self, token) -> None:
         name, start = token
-        end = torch.cuda.Event(enable_timing=True)
+        end = self._event()
         end.record()
         self._events.setdefault(name, []).append((start, end))
 
