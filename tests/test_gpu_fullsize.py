@@ -309,3 +309,61 @@ def test_one_rank_shard_step_and_cast_on_gather():
     want = full[:lay.numel].to(torch.bfloat16)
     got = torch.cat([t.reshape(-1) for t in params16])
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_llama3_8b_whole_model_one_rank_flat_indices_beyond_2_32():
+    """All of Llama-3-8B (8,030,261,248 params, 291 tensors) as one group at
+    world size 1, bf16, ZeRO-3: the flat indices run past 2^32, so every
+    index computation of the kernels is exercised in 64 bits.  One
+    boundary: the norm against a float64 sum of squares, a million random
+    elements (about half beyond 2^32) bit-exact against the kernel recipe,
+    the bf16 model copy the round-to-nearest-even cast of the masters."""
+    shapes = shapes_of("llama3-8b")
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    params = [nn.Parameter((torch.randn(*s, generator=gen, device=DEV) * 0.02).to(torch.bfloat16))
+              for s in shapes]
+    mod = nn.ParameterList(params)
+    engine = ms.initialize(model=mod, model_parameters=list(mod), config=_cfg("bf16", 3))
+    g = engine.flat_groups[0]
+    n = g.numel
+    assert n == 8_030_261_248 and n > 2 ** 32 and g.whole_range
+    offsets = np.array(g.layout.offsets, dtype=np.int64)
+    rng = np.random.default_rng(1)
+    idx = np.unique(np.concatenate([rng.integers(0, n, size=1_000_000),
+                                    np.array([0, 2 ** 32 - 1, 2 ** 32, 2 ** 32 + 1, n - 1])]))
+    assert (idx >= 2 ** 32).sum() > 400_000
+    pi = np.searchsorted(offsets, idx, side="right") - 1
+    local = idx - offsets[pi]
+    idx_t = torch.from_numpy(idx).to(DEV)
+
+    def gather(tensors):
+        out = np.empty(len(idx), dtype=np.float32)
+        for k in np.unique(pi):
+            sel = np.nonzero(pi == k)[0]
+            t = tensors[k].detach().reshape(-1)
+            out[sel] = t[torch.from_numpy(local[sel]).to(DEV)].float().cpu().numpy()
+        return out
+
+    engine.optimizer.gather_parameters()               # what the forward does
+    grads = _grads(shapes, torch.bfloat16, gen, std=1e-4)
+    p0 = g.data[idx_t].cpu().numpy()
+    m0 = engine.optimizer.state[0]["exp_avg"][idx_t].cpu().numpy()
+    v0 = engine.optimizer.state[0]["exp_avg_sq"][idx_t].cpu().numpy()
+    g_s = gather(grads)
+    exact = sum(float(t.double().pow(2).sum()) for t in grads)
+    for p, gr in zip(params, grads):
+        p.grad = gr
+    del grads
+    engine.micro_steps += 1
+    assert engine.step() is True
+    sc = engine.last_boundary
+    assert not sc.overflow and sc.clip_applied == 1
+    assert abs(engine.grad_norm - np.sqrt(exact)) <= 1e-6 * np.sqrt(exact)
+    wp, wm, wv = recipe.adamw_step(p0, m0, v0, g_s, lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+                                   wd=0.01, step=1, clip_coef=float(np.float32(sc.coef)))
+    np.testing.assert_array_equal(g.data[idx_t].cpu().numpy().view(np.int32), wp.view(np.int32))
+    np.testing.assert_array_equal(engine.optimizer.state[0]["exp_avg"][idx_t].cpu().numpy(), wm)
+    np.testing.assert_array_equal(engine.optimizer.state[0]["exp_avg_sq"][idx_t].cpu().numpy(), wv)
+    assert not engine.optimizer.params_gathered
+    model = gather(params)                              # the freed placeholders
+    np.testing.assert_array_equal(model, torch.from_numpy(wp).to(torch.bfloat16).float().numpy())
