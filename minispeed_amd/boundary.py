@@ -80,6 +80,7 @@ class Workspace:
         self._side = torch.cuda.Stream(device)
         self._k2_done = torch.cuda.Event()
         self._copied = torch.cuda.Event()
+        self._stream: Optional[torch.cuda.Stream] = None   # stream of the last boundary
 
     def partial_ptrs(self, g: int):
         off = g * self.nblk
@@ -93,6 +94,16 @@ class Workspace:
         self.host.copy_(self.scalars, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
         return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
+
+    def enter(self) -> None:
+        """Called at the start of a boundary.  Kernels of the previous
+        boundary (K3 reading the scalars and segment tables this boundary
+        overwrites) may still run on its stream; if the current stream is
+        another one, it first waits for everything queued there."""
+        cur = torch.cuda.current_stream(self.device)
+        if self._stream is not None and self._stream != cur:
+            cur.wait_stream(self._stream)
+        self._stream = cur
 
     def start_readback(self) -> None:
         """Queue the copy of K2's scalars (just launched on the current
@@ -200,6 +211,7 @@ def run_boundary(
     """
     lib = _native.load()
     device = ws.device
+    ws.enter()
     stream = _native.stream_handle(device)
     scale = float(scaler.loss_scale_factor)
     unscale = scale != 1.0

@@ -192,9 +192,11 @@ class SegmentTable:
     through a fresh pinned host tensor with a non-blocking copy on the
     current stream, replacing the least recently used entry; torch's host
     allocator keeps the staging memory until the copy has run, and the copy
-    is stream-ordered before the kernels that read the table.  Entries are
-    only replaced between boundaries, which end with a stream
-    synchronisation, so no kernel still reads a replaced entry.
+    is stream-ordered before the kernels that read the table.  The copy
+    that overwrites a replaced entry is queued on the stream of the
+    boundary that uploads it, after every kernel of the earlier boundaries
+    that read the entry: the boundaries of one engine run on one stream, or
+    the new stream first waits for the old one (``Workspace.enter``).
     """
 
     SLOTS = 4

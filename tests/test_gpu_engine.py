@@ -319,3 +319,31 @@ def test_two_param_groups_with_own_hyperparameters():
     train(engine, x, y, 2, GAS)
     assert engine.global_steps == 2
     assert all(st["step"] == 2 for st in engine.optimizer.state)
+
+
+def test_boundaries_on_alternating_streams_match_one_stream():
+    """step() returns before K3 finishes; a boundary issued on another
+    stream must still see the previous one complete (Workspace.enter)."""
+    x, y = make_batch(4, GAS, MICRO)
+    results = []
+    for alternate in (False, True):
+        model = build_model()
+        engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                               config=config(dtype="fp16", lr=1e-2))
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        for s in range(4):
+            for m in range(GAS):
+                engine.backward(mse(engine(x[s, m]), y[s, m]))
+            if alternate:
+                st = streams[s % 2]
+                st.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(st):
+                    assert engine.step() is True
+                torch.cuda.current_stream().wait_stream(st)
+            else:
+                assert engine.step() is True
+        torch.cuda.synchronize()
+        results.append((engine.flat_groups[0].data.clone(), engine.optimizer.state[0]["exp_avg_sq"].clone(),
+                        engine.grad_norm))
+    assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])
+    assert results[0][2] == results[1][2]
