@@ -165,7 +165,11 @@ def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
                    f"({total:,} params: {what}); median of 3 steps after 1 warm-up, "
                    f"{med * 1e3:.0f} ms/step; {threads} threads of {os.cpu_count()} on "
                    f"{cpu_model()}"),
+        # effective GB/s at the fused path's 30 B/param, the materialized
+        # 36 B/param and the ~150 B/param the unfused torch sequence moves
         "gbps_at_30_bytes": round(30 * total / med / 1e9, 2),
+        "gbps_at_36_bytes": round(36 * total / med / 1e9, 2),
+        "gbps_at_150_bytes": round(150 * total / med / 1e9, 2),
     }
 
 
