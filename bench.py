@@ -236,7 +236,7 @@ def bench_llama_shard(args) -> dict:
         if t:
             t.stop(tok)
         _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 1.0, 0, 1.0,
-                                       0, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), stream),
+                                       0, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), None, stream),
                       "ms_norm_clip")
         tok = t.start("k3") if t else None
         _native.check(lib.ms_fused_adamw(master.data_ptr(), m.data_ptr(), v.data_ptr(), None,

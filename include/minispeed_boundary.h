@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MS_ABI_VERSION 1
+#define MS_ABI_VERSION 2
 
 /* element types of ragged gradient / model storage */
 enum {
@@ -161,13 +161,17 @@ int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
  * coef64 = max_norm / (norm + 1e-6) and clip_applied = (coef64 != 1).
  * The scaler fields are the state before this boundary.
  * out [dev] receives an ms_step_scalars_t.
+ * out_host [pinned host memory, optional] receives the same struct, made
+ * visible to the host before the kernel completes: the caller records an
+ * event after this call and reads out_host once the event has completed,
+ * with no copy (the one read-back of engine.py:278-322's two syncs).
  */
 int ms_norm_clip(const double* block_sumsq, const uint32_t* block_flag,
                  int32_t nblk, int32_t ngroups, int32_t has_clip,
                  double max_norm, int32_t scaler_enabled, double scale,
                  int64_t good_steps, int64_t skipped_steps, int64_t window,
                  double min_scale, double max_scale, ms_step_scalars_t* out,
-                 void* stream);
+                 ms_step_scalars_t* out_host, void* stream);
 
 /*
  * K3 — fused AdamW over the owned range [begin, end) plus the cast of the

@@ -19,7 +19,7 @@ from typing import Optional
 import torch  # noqa: F401  (must precede the dlopen below, see module doc)
 
 LIB_NAME = "libminispeed_boundary.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -102,7 +102,7 @@ SIGNATURES = {
     ),
     "ms_norm_clip": (
         ctypes.c_int,
-        [_P, _P, _I32, _I32, _I32, _D, _I32, _D, _I64, _I64, _I64, _D, _D, _P, _P],
+        [_P, _P, _I32, _I32, _I32, _D, _I32, _D, _I64, _I64, _I64, _D, _D, _P, _P, _P],
     ),
     "ms_fused_adamw": (
         ctypes.c_int,

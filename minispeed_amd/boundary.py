@@ -73,13 +73,12 @@ class Workspace:
         self.partials = torch.empty(n, dtype=torch.float64, device=device)
         self.flags = torch.empty(n, dtype=torch.int32, device=device)
         self.scalars = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=device)
+        # K2 also writes its result here (pinned host memory the device
+        # writes directly), so the read-back is a wait on an event recorded
+        # after K2: no copy, and K3, queued behind K2, keeps running while
+        # the host does its bookkeeping
         self.host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
-        # the read-back runs on a side stream (default priority) that waits
-        # for K2 only, so K3 is not queued behind the copy and the host's
-        # bookkeeping overlaps K3
-        self._side = torch.cuda.Stream(device)
         self._k2_done = torch.cuda.Event()
-        self._copied = torch.cuda.Event()
         self._stream: Optional[torch.cuda.Stream] = None   # stream of the last boundary
 
     def partial_ptrs(self, g: int):
@@ -106,18 +105,14 @@ class Workspace:
         self._stream = cur
 
     def start_readback(self) -> None:
-        """Queue the copy of K2's scalars (just launched on the current
-        stream) to pinned memory on the side stream."""
-        self._k2_done.record(torch.cuda.current_stream(self.device))
-        self._side.wait_event(self._k2_done)
-        with torch.cuda.stream(self._side):
-            self.host.copy_(self.scalars, non_blocking=True)
-            self._copied.record(self._side)
+        """Mark the end of K2 (just launched on the current stream with
+        ``host`` as its host-side output)."""
+        self._k2_done.record(self._stream)
 
     def finish_readback(self) -> _native.StepScalars:
-        """Wait for the copy queued by :meth:`start_readback` (K2 and the
-        copy only; later kernels on the current stream keep running)."""
-        self._copied.synchronize()
+        """Wait for K2 (later kernels on the stream keep running) and read
+        the scalars it wrote to pinned host memory."""
+        self._k2_done.synchronize()
         return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
 
 
@@ -199,8 +194,9 @@ def run_boundary(
 ) -> _native.StepScalars:
     """Launch the whole boundary and return K2's scalars (one host sync).
 
-    K1 and K2 are launched as soon as the gradient addresses are known and
-    the copy of K2's scalars is queued on a side stream; ``model_targets()``
+    K1 and K2 are launched as soon as the gradient addresses are known (K2
+    writes its scalars to device memory for K3 and to pinned host memory
+    for the host) and an event marks K2's end; ``model_targets()``
     (the addresses K3 casts the updated masters into, per group; ``None`` for
     no write) is called after that, so whatever it does on the host overlaps
     K1 on the device.  The function returns once K2's scalars are on the
@@ -250,7 +246,7 @@ def run_boundary(
         1 if scaler.enabled else 0, float(scaler.scale), int(scaler.good_steps),
         int(scaler.skipped_steps), int(scaler.scale_window),
         float(scaler.min_scale), float(scaler.max_scale),
-        ws.scalars.data_ptr(), stream,
+        ws.scalars.data_ptr(), ws.host.data_ptr(), stream,
     )
     timer.stop(tok)
     _native.check(rc, "ms_norm_clip")
@@ -302,5 +298,5 @@ def scan_nonfinite(buf: torch.Tensor) -> bool:
     _native.check(lib.ms_grad_stats(dev_table.data_ptr(), 1, dtype, 0, n, 0, 0, 0, 1.0,
                                     None, psum, pflag, ws.nblk, stream), "ms_grad_stats")
     _native.check(lib.ms_norm_clip(psum, pflag, ws.nblk, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0,
-                                   ws.scalars.data_ptr(), stream), "ms_norm_clip")
+                                   ws.scalars.data_ptr(), None, stream), "ms_norm_clip")
     return bool(ws.read_scalars().overflow)

@@ -403,7 +403,8 @@ __global__ __launch_bounds__(kNormThreads) void k_norm_clip(
     const double* __restrict__ bsum, const uint32_t* __restrict__ bflag,
     int nblk, int ngroups, int has_clip, double max_norm, int scaler_enabled,
     double scale, int64_t good_steps, int64_t skipped_steps, int64_t window,
-    double min_scale, double max_scale, ms_step_scalars_t* __restrict__ out) {
+    double min_scale, double max_scale, ms_step_scalars_t* __restrict__ out,
+    ms_step_scalars_t* __restrict__ out_host) {
   constexpr int kNormWaves = kNormThreads / 64;
   __shared__ double wsum[kNormWaves];
   __shared__ uint32_t wbad[kNormWaves];
@@ -479,6 +480,12 @@ __global__ __launch_bounds__(kNormThreads) void k_norm_clip(
   r.next_good_steps = good;
   r.next_skipped_steps = skipped;
   *out = r;
+  if (out_host) {
+    // the host's copy, in pinned host memory: made visible system-wide
+    // before the kernel (and the event the host waits on) completes
+    *out_host = r;
+    __threadfence_system();
+  }
 }
 
 // ------------------------------------------------------------------ K3
@@ -855,7 +862,7 @@ int ms_norm_clip(const double* block_sumsq, const uint32_t* block_flag,
                  double max_norm, int32_t scaler_enabled, double scale,
                  int64_t good_steps, int64_t skipped_steps, int64_t window,
                  double min_scale, double max_scale, ms_step_scalars_t* out,
-                 void* stream) {
+                 ms_step_scalars_t* out_host, void* stream) {
   if (!block_sumsq || !block_flag || !out || ngroups < 0) return MS_EINVAL;
   if (nblk < kStatsBlocks) return MS_EBLOCKS;
   if (window < 1) return MS_EINVAL;
@@ -863,7 +870,7 @@ int ms_norm_clip(const double* block_sumsq, const uint32_t* block_flag,
   hipLaunchKernelGGL(k_norm_clip, dim3(1), dim3(kNormThreads), 0, st, block_sumsq,
                      block_flag, nblk, ngroups, has_clip, max_norm,
                      scaler_enabled, scale, good_steps, skipped_steps, window,
-                     min_scale, max_scale, out);
+                     min_scale, max_scale, out, out_host);
   return launch_status();
 }
 

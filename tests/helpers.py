@@ -104,7 +104,7 @@ def k2(psum: np.ndarray, pflag: np.ndarray, ngroups=1, has_clip=False, max_norm=
     en, scale, good, skipped, window, mn, mx = scaler
     rc = lib.ms_norm_clip(ps.data_ptr(), pf.data_ptr(), nb, ngroups, 1 if has_clip else 0,
                           float(max_norm), 1 if en else 0, float(scale), int(good), int(skipped),
-                          int(window), float(mn), float(mx), out.data_ptr(), stream())
+                          int(window), float(mn), float(mx), out.data_ptr(), None, stream())
     _native.check(rc, "ms_norm_clip")
     torch.cuda.synchronize()
     return _native.StepScalars.from_buffer_copy(out.cpu().numpy().tobytes())

@@ -277,7 +277,7 @@ def test_one_rank_shard_step_and_cast_on_gather():
     _native.check(lib.ms_grad_stats(tdev.data_ptr(), len(table), _native.DTYPE_BF16, lo, hi, lo, hi,
                                     0, 1.0, None, psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
     _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 0.05, 0, 1.0, 0, 0,
-                                   1000, 1.0, 2.0 ** 24, scal.data_ptr(), st), "k2")
+                                   1000, 1.0, 2.0 ** 24, scal.data_ptr(), None, st), "k2")
     hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 4)
     _native.check(lib.ms_fused_adamw(master.data_ptr(), m.data_ptr(), v.data_ptr(), None,
                                      tdev.data_ptr(), len(table), _native.DTYPE_BF16,

@@ -21,7 +21,7 @@ from oracle import boundary as ob
 from oracle import recipe
 from tests.helpers import (DEV, HALF_SPECIALS, Table, adamw_params, bits, k1, k2, k3, k4,
                            layout_for, master_step_within_ulps, ragged_grads, scalars_device,
-                           set_bits, store)
+                           set_bits, store, stream)
 
 pytestmark = pytest.mark.gpu
 
@@ -288,3 +288,26 @@ def test_k4_cast_matches_torch_rounding(mdtype):
     want = torch.from_numpy(flat[:lay.numel]).to(mdtype)
     got = torch.cat([t.reshape(-1).cpu() for t in models])
     np.testing.assert_array_equal(bits(got), bits(want))
+
+
+def test_k2_host_copy_equals_device_result_after_an_event():
+    """K2's optional host-side output (pinned memory written by the kernel)
+    holds the device result once an event recorded after K2 completes."""
+    lib = _native.load()
+    nb = _native.stats_blocks()
+    rng = np.random.default_rng(3)
+    ps = torch.from_numpy(rng.random(nb) * 1e-2).to(DEV)
+    pf = torch.zeros(nb, dtype=torch.int32, device=DEV)
+    out = torch.zeros(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
+    host = torch.full((_native.SCALARS_BYTES,), 0xAB, dtype=torch.uint8, pin_memory=True)
+    for k, flag in enumerate((0, 1, 0)):
+        pf[17] = flag
+        ev = torch.cuda.Event()
+        rc = lib.ms_norm_clip(ps.data_ptr(), pf.data_ptr(), nb, 1, 1, 0.5, 1, 2.0 ** 16, k, 0, 1000,
+                              1.0, 2.0 ** 24, out.data_ptr(), host.data_ptr(), stream())
+        _native.check(rc, "ms_norm_clip")
+        ev.record()
+        ev.synchronize()
+        got = _native.StepScalars.from_buffer_copy(host.numpy().tobytes())
+        assert host.numpy().tobytes() == out.cpu().numpy().tobytes()
+        assert got.overflow == flag and got.next_good_steps == (0 if flag else k + 1)

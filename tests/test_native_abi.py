@@ -88,9 +88,11 @@ def test_host_argument_errors_return_codes_without_launching():
     assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb - 1, None) == EBLOCKS
     assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb, None) == ETABLE
     assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 1, 0.0, 8, None, None, nb, None) == ETABLE
-    assert lib.ms_norm_clip(None, None, nb, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, None, None) == EINVAL
-    assert lib.ms_norm_clip(8, 8, nb - 1, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None) == EBLOCKS
-    assert lib.ms_norm_clip(8, 8, nb, 1, 0, 0.0, 0, 1.0, 0, 0, 0, 1.0, 1.0, 8, None) == EINVAL
+    assert lib.ms_norm_clip(None, None, nb, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, None, None,
+                            None) == EINVAL
+    assert lib.ms_norm_clip(8, 8, nb - 1, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None,
+                            None) == EBLOCKS
+    assert lib.ms_norm_clip(8, 8, nb, 1, 0, 0.0, 0, 1.0, 0, 0, 0, 1.0, 1.0, 8, None, None) == EINVAL
     hp = _native.AdamWParams()
     assert lib.ms_fused_adamw(8, 8, 8, None, None, 0, 9, 1, 0, 10, ctypes.byref(hp), 8, None) == EINVAL
     assert lib.ms_fused_adamw(8, 8, 8, None, None, 0, 1, 1, 0, 10, None, 8, None) == EINVAL
