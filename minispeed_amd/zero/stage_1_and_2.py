@@ -148,6 +148,3 @@ class ZeROOptimizer:
     def load_state_dict(self, state: dict) -> None:
         self.adam.load_state_dict(state)
 
-    def _grad_device(self) -> torch.device:
-        return self.flat_groups[0].device
-
