@@ -10,12 +10,14 @@ clip 1.0, 20 boundaries of one micro-batch of 8 x 128 tokens.
   the clip coefficients agree, masters within 2 fp32 ulp per step.
 * The whole run is compared with minispeed's own run of the same model,
   initialisation and token batches on the CPU (``cases.json`` key
-  ``tinylm``, written by tests/golden/make_golden.py): losses within 2e-6
-  relative, gradient norms within 1e-5 relative, per-tensor parameter sums
-  of squares within 3e-5 relative and sums within 1e-4 of their L2 scale.
+  ``tinylm``, written by tests/golden/make_golden.py): losses within 2e-5
+  relative, gradient norms within 1e-4 relative, per-tensor parameter sums
+  of squares within 1e-4 relative and sums within 2e-4 of their L2 scale.
   These tolerances cover the different reduction orders of the CPU and GPU
   forward/backward kernels, which is the only difference between the runs
-  (measured: 1.5e-7, 6.5e-7, 3.0e-6 and 1.7e-5).
+  (measured: 1.5e-7, 6.5e-7, 3.0e-6 and 1.7e-5; the margin allows for other
+  GEMM algorithm choices on another box, and stays far below what a wrong
+  boundary step does to a 20-step run).
 """
 
 from __future__ import annotations
@@ -88,11 +90,11 @@ def test_tiny_lm_trains_through_the_engine_and_matches_the_oracle_and_minispeed(
     assert engine.global_steps == trace["global_steps"] == trace["steps"]
 
     # against minispeed's own CPU run
-    np.testing.assert_allclose(losses, trace["losses"], rtol=2e-6)
-    np.testing.assert_allclose(norms, trace["grad_norms"], rtol=1e-5)
+    np.testing.assert_allclose(losses, trace["losses"], rtol=2e-5)
+    np.testing.assert_allclose(norms, trace["grad_norms"], rtol=1e-4)
     for name, p in model.named_parameters():
         s, sq = trace["param_sum_sumsq"][name]
         got = p.detach().double()
-        assert abs(float(got.pow(2).sum()) - sq) <= 3e-5 * sq, name
+        assert abs(float(got.pow(2).sum()) - sq) <= 1e-4 * sq, name
         scale = math.sqrt(sq * p.numel())
-        assert abs(float(got.sum()) - s) <= 1e-4 * max(scale, 1e-12), name
+        assert abs(float(got.sum()) - s) <= 2e-4 * max(scale, 1e-12), name
