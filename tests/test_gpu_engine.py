@@ -347,3 +347,54 @@ def test_boundaries_on_alternating_streams_match_one_stream():
                         engine.grad_norm))
     assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])
     assert results[0][2] == results[1][2]
+
+
+def test_thousands_of_tiny_tensors_against_the_oracle():
+    """3000 parameters of 1..300 elements (segment tables of thousands of
+    rows, most tiles straddling segment edges), fp16, ZeRO-2, clip: every
+    boundary against the oracle started from the GPU's own state."""
+    from oracle import boundary as ob
+    from oracle import recipe
+    from tests.helpers import master_step_within_ulps
+
+    rng = np.random.default_rng(5)
+    sizes = rng.integers(1, 301, size=3000)
+    gen = torch.Generator().manual_seed(9)
+    init = [torch.randn(int(n), generator=gen) * 0.02 for n in sizes]
+    params = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    module = nn.ParameterList(params)
+    engine = ms.initialize(model=module, model_parameters=list(module),
+                           config=config(dtype="fp16", stage=2, lr=1e-3, power=12, gas=1))
+    ref_params = [nn.Parameter(t.clone()) for t in init]
+    ref = ob.Engine([ref_params], [{"lr": 1e-3, "betas": (0.9, 0.999), "eps": 1e-8,
+                                    "weight_decay": 0.01}], dtype="fp16", zero_stage=2, clip=1.0,
+                    initial_scale_power=12, loss_scale_window=100,
+                    scheduler_params={"warmup_max_lr": 1e-3})
+    g = engine.flat_groups[0]
+    assert len(g.boundary_table(0, g.numel_padded, g.grad_pointers()[0], None)) >= 3000
+    for step in range(3):
+        grads = [(torch.randn(int(n), generator=gen) * 1e-2 * 2.0 ** 12).half() for n in sizes]
+        before = g.data.detach().cpu()
+        st = engine.optimizer.state[0]
+        ref.load_state([before], [st["exp_avg"].cpu()], [st["exp_avg_sq"].cpu()], [st["step"]],
+                       (engine.loss_scaler.scale, engine.loss_scaler.good_steps,
+                        engine.loss_scaler.skipped_steps),
+                       engine.lr_scheduler.last_epoch, [pg["lr"] for pg in engine.optimizer.param_groups])
+        for p, rp, gr in zip(params, ref_params, grads):
+            p.grad = gr.to(DEV)
+            rp.grad = gr.clone()
+        engine.micro_steps += 1
+        ref.micro_steps += 1
+        assert engine.step() is True and ref.step() is True
+        assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
+        _, _, coef = recipe.clip_coef(np.float32(ref.grad_norm), 1.0)
+        same = np.float32(engine.last_boundary.coef) == np.float32(coef)
+        ok, worst = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
+                                            ref.groups[0].data.numpy(), 2.0 if same else 4.0)
+        assert ok, (step, worst)
+        if same:
+            assert torch.equal(st["exp_avg"].cpu(), ref.state[0]["exp_avg"])
+        master = g.data.cpu()
+        for (off, p), n in zip(g._offsets, g._numels):
+            assert torch.equal(p.detach().cpu().view(torch.int16),
+                               master[off:off + n].to(torch.float16).view(torch.int16))
