@@ -11,6 +11,8 @@ the only difference being torch's CPU sqrt.
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -311,3 +313,63 @@ def test_k2_host_copy_equals_device_result_after_an_event():
         got = _native.StepScalars.from_buffer_copy(host.numpy().tobytes())
         assert host.numpy().tobytes() == out.cpu().numpy().tobytes()
         assert got.overflow == flag and got.next_good_steps == (0 if flag else k + 1)
+
+
+def test_boundary_kernels_replay_in_a_hip_graph():
+    """K1 -> K2 -> K3 captured once in a graph and replayed from the same
+    starting state several times, with eager work and synchronisations in
+    between, gives the eager result every time (no memset nodes, no host
+    sync inside; K1 zero-fills its partial slots itself)."""
+    lib = _native.load()
+    shapes = RAGGED
+    grads = _device(ragged_grads(shapes, F16, 1e-2, seed=77, scale=1024.0))
+    lay = layout_for([int(np.prod(s)) for s in shapes])
+    n = lay.numel_padded
+    models = [torch.empty(int(np.prod(s)), dtype=F16, device=DEV) for s in shapes]
+    table = Table(lay, 0, n, [store(g, off) for g, off in zip(grads, lay.offsets)],
+                  [store(m, off) for m, off in zip(models, lay.offsets)])
+    nb = _native.stats_blocks()
+    psum = torch.empty(nb, dtype=torch.float64, device=DEV)
+    pflag = torch.empty(nb, dtype=torch.int32, device=DEV)
+    scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    p0 = torch.randn(n, generator=gen, device=DEV) * 0.02
+    m0 = torch.randn(n, generator=gen, device=DEV) * 1e-3
+    v0 = torch.rand(n, generator=gen, device=DEV) * 1e-6
+    p, m, v = p0.clone(), m0.clone(), v0.clone()
+    hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 7, grad_scale=1024.0, unscale=True)
+
+    def boundary(st):
+        _native.check(lib.ms_grad_stats(table.ptr, table.nseg, _native.DTYPE_F16, 0, n, 0, n, 1,
+                                        1024.0, None, psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
+        _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 0.5, 1, 1024.0,
+                                       3, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), None, st), "k2")
+        _native.check(lib.ms_fused_adamw(p.data_ptr(), m.data_ptr(), v.data_ptr(), None, table.ptr,
+                                         table.nseg, _native.DTYPE_F16, _native.DTYPE_F16, 0, n,
+                                         ctypes.byref(hp), scal.data_ptr(), st), "k3")
+
+    boundary(stream())
+    torch.cuda.synchronize()
+    want = [t.clone() for t in (p, m, v, scal)] + [torch.cat(models).clone()]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        for t, t0 in ((p, p0), (m, m0), (v, v0)):
+            t.copy_(t0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            boundary(side.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for t, t0 in ((p, p0), (m, m0), (v, v0)):
+            t.copy_(t0)
+        psum.fill_(float("nan"))          # eager work between replays
+        scal.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [p, m, v, scal, torch.cat(models)]
+        for a, b in zip(got, want):
+            assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), rep
