@@ -31,6 +31,7 @@ from . import checkpoint as ckpt
 from .config import DeepSpeedConfig, load_config
 from .contiguous import ContiguousGradients
 from .flat import FlatParamGroup, build_flat_groups
+from .flat import _walk as flat_walk
 from .optim import build_scheduler
 from .precision import DynamicLossScaler
 from .utils import Timers
@@ -79,7 +80,9 @@ class DeepSpeedEngine:
             raise RuntimeError(
                 f"device {self.device}: the boundary step runs as HIP kernels on a ROCm GPU"
             )
-        _native.load()  # fail now, not at the first boundary, if the library is missing
+        # fail now, not at the first boundary, if a native part is missing
+        _native.load()
+        flat_walk()
         self.timers = Timers()
         self.module = model.to(self.device)
 
