@@ -468,6 +468,9 @@ def main(argv=None) -> int:
         },
         "hbm_gbps": round(step_gbps, 1),
         "hbm_frac": round(step_gbps / PEAK_GBPS, 4),
+        # the same step rate at the 36 B/param of a path that materializes
+        # the fp32 flat gradient (the accounting of the 80%-of-peak target)
+        "hbm_gbps_at_36_bytes": round(36 * n_params / (ms_step * 1e-3) / 1e9, 1),
         "kernel_ms": {k: round(v, 4) for k, v in k_ms.items()},
         "roofline": {
             "kernel": "K3 k_adamw (fused AdamW + model cast)",
