@@ -325,7 +325,7 @@ def traffic_for(kernel: str, workload: str, grad_dtype: str, mode: str):
 def main(argv=None) -> int:
     args = parse(argv)
     if args.gpus != 1:
-        print(json.dumps({"error": f"--gpus {args.gpus}: this build measures the boundary step on one "
+        print(json.dumps({"error": f"--gpus {args.gpus}: bench.py measures the boundary step on one "
                                    "GPU; multi-GPU runs are not part of it"}))
         return 2
     import numpy as np

@@ -6,7 +6,7 @@ behaviour: rank/world come from the environment when no process group exists
 (so a ``FlatParamGroup`` can be built as "rank r of W" for one rank's shard),
 collectives are identities, the world-1 reduce-scatter / all-gather are
 copies.  Starting a multi-process job is rejected: the RCCL exchange of a
-multi-GPU boundary step is not part of this build.
+multi-GPU boundary step is not implemented in this package.
 """
 
 from __future__ import annotations
@@ -77,7 +77,7 @@ def init_distributed() -> None:
     """Accept a world of one; refuse anything larger."""
     if is_distributed() or get_world_size() > 1:
         raise MultiGPUNotSupported(
-            f"world_size={get_world_size()}: this build runs one rank on one GPU; "
+            f"world_size={get_world_size()}: minispeed_amd runs one rank on one GPU; "
             "the multi-GPU exchange (reduce-scatter, norm partials, all-gather) "
             "is not implemented"
         )

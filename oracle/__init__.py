@@ -2,8 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in ``minispeed_amd`` imports this
 package; only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, as the checker (and, for
-``bench.py``, as the timed CPU baseline), never as the thing measured.
+``cpu_baseline`` leg of ``bench.py`` use it: as the expected result the GPU
+path is compared with (and, for ``bench.py``, as the timed CPU baseline),
+never as the thing measured.
 
 Modules
   boundary   torch-CPU restatement of the reference op sequence

@@ -2,7 +2,8 @@
 
     python tests/golden/make_golden.py [--reference /root/reference]
 
-Runs in the build container only (the reference never travels).  It imports
+Runs only where minispeed's sources are (they never travel with this
+repository; the fixtures do).  It imports
 the reference package from ``--reference`` and drives its CPU engine
 (``MINISPEED_DEVICE=cpu``) through seeded cases that exercise the hot path:
 ragged parameter lists, fp16 / bf16 / fp32, ZeRO stages 0-3 at world size 1,
