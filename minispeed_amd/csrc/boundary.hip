@@ -43,6 +43,10 @@ namespace {
 constexpr int kThreads = 128;
 constexpr int kVec = 8;                   // elements per lane per tile
 constexpr int kTile = kThreads * kVec;    // 1024 flat elements
+// K4 (2 B read : 1 B written) prefers 4 wave64 per block: 64 / 128 / 256 /
+// 512 threads take 8.09 / 8.16 / 8.00 / 8.11 ms for the 8B-param cast.
+constexpr int kCastThreads = 256;
+constexpr int kCastTile = kCastThreads * kVec;   // 2048 flat elements
 constexpr int kStatsBlocks = 16384;       // K1 partial slots per group
 #ifndef MS_STATS_MIN_CHUNK
 #define MS_STATS_MIN_CHUNK 32768
@@ -602,19 +606,19 @@ __global__ __launch_bounds__(kThreads) void k_adamw(
 
 // ------------------------------------------------------------------ K4
 template <class M>
-__global__ __launch_bounds__(kThreads) void k_cast(
+__global__ __launch_bounds__(kCastThreads) void k_cast(
     const float* __restrict__ flat, const ms_segment_t* __restrict__ segs,
     int nseg, int64_t begin, int64_t end) {
   const int lane = threadIdx.x;
   const int64_t n = end - begin;
-  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const int64_t ntiles = (n + kCastTile - 1) / kCastTile;
   const bool flat_vec = aligned16(flat);
   for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    const int64_t t0 = begin + t * kTile;
-    const int64_t t1 = (t0 + kTile < end) ? t0 + kTile : end;
+    const int64_t t0 = begin + t * kCastTile;
+    const int64_t t1 = (t0 + kCastTile < end) ? t0 + kCastTile : end;
     const int s = find_seg(segs, nseg, t0);
     const ms_segment_t seg = segs[s];
-    const bool fast = t1 - t0 == kTile && t0 >= seg.begin && t1 <= seg_end(seg) && flat_vec &&
+    const bool fast = t1 - t0 == kCastTile && t0 >= seg.begin && t1 <= seg_end(seg) && flat_vec &&
                       ((t0 - seg.begin) & (kVec - 1)) == 0 &&
                       aligned16(seg.model);
     const int64_t i0 = t0 + static_cast<int64_t>(lane) * kVec;
@@ -947,9 +951,9 @@ int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
   if (!flat) return MS_EINVAL;
   if (!segs || nseg <= 0 || nseg > kMaxSegs) return MS_ETABLE;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t ntiles = (end - begin + kTile - 1) / kTile;
+  const int64_t ntiles = (end - begin + kCastTile - 1) / kCastTile;
   const dim3 grid(stream_grid(ntiles, env_int("MS_CAST_BLOCKS_PER_CU", 0)));
-  const dim3 block(kThreads);
+  const dim3 block(kCastThreads);
   switch (model_dtype) {
     case MS_DTYPE_F32:
       hipLaunchKernelGGL(k_cast<DF32>, grid, block, 0, st, flat, segs, nseg,
