@@ -373,3 +373,89 @@ def test_boundary_kernels_replay_in_a_hip_graph():
         got = [p, m, v, scal, torch.cat(models)]
         for a, b in zip(got, want):
             assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), rep
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_layouts_with_misaligned_views_and_empty_params(seed):
+    """Random ragged lists (some zero-size), every gradient and model copy a
+    view at a random element offset of one pool (so most addresses are not
+    16-byte aligned), a random owned range: K1's flags / sum of squares /
+    flat gradient, K3 against the recipe bit for bit (elements outside the
+    range untouched) and K4's casts against torch."""
+    rng = np.random.default_rng(100 + seed)
+    gdtype = [F16, BF16, F32][seed % 3]
+    sizes = [int(x) for x in rng.integers(0, 3000, size=14)]
+    sizes[int(rng.integers(0, 14))] = 0
+    sizes[0] = max(sizes[0], 1)
+    lay = layout_for(sizes)
+    n = lay.numel_padded
+    lo = int(rng.integers(0, n // 3))
+    hi = int(rng.integers(2 * n // 3, n + 1))
+    gen = torch.Generator().manual_seed(seed)
+
+    def pool_views(dtype, fill):
+        pool = torch.full((sum(sizes) + 8 * len(sizes) + 8,), fill, dtype=dtype, device=DEV)
+        views, pos = [], int(rng.integers(0, 8))
+        for k in sizes:
+            views.append(pool[pos:pos + k])
+            pos += k + int(rng.integers(0, 8))
+        return pool, views
+
+    gpool, gviews = pool_views(gdtype, 0.0)
+    grads_cpu = []
+    for view, k in zip(gviews, sizes):
+        gcpu = (torch.randn(k, generator=gen) * 1e-2).to(gdtype)
+        view.copy_(gcpu.to(DEV))
+        grads_cpu.append(gcpu)
+    if seed == 4 and sizes[3] > 0:
+        gviews[3][0] = float("nan")
+        grads_cpu[3][0] = float("nan")
+    gst = [(v.data_ptr(), (off, off + k), v.element_size()) if k else None
+           for v, off, k in zip(gviews, lay.offsets, sizes)]
+    flat_want = np.zeros(n, np.float32)
+    for gcpu, off, k in zip(grads_cpu, lay.offsets, sizes):
+        flat_want[off:off + k] = gcpu.float().numpy()
+
+    # K1: flat gradient, flags, owned-range sum of squares
+    tab1 = Table(lay, 0, n, gst, [None] * len(sizes))
+    flat = torch.full((n,), 7.0, device=DEV)
+    psum, pflag = k1(tab1, gdtype, 0, n, lo, hi, flat=flat)
+    np.testing.assert_array_equal(flat.cpu().numpy().view(np.int32), flat_want.view(np.int32))
+    assert bool(pflag.any()) == (seed == 4 and sizes[3] > 0)
+    if seed != 4:
+        exact = recipe.sumsq_f64(flat_want[lo:hi])
+        assert abs(psum.sum() - exact) <= 1e-12 * max(exact, 1e-300)
+        # K3 over [lo, hi) with misaligned model copies
+        mpool, mviews = pool_views(gdtype, 3.0)
+        mst = [(v.data_ptr(), (off, off + k), v.element_size()) if k else None
+               for v, off, k in zip(mviews, lay.offsets, sizes)]
+        tab3 = Table(lay, lo, hi, gst, mst)
+        p = rng.normal(0, 0.02, hi - lo).astype(np.float32)
+        m = rng.normal(0, 1e-3, hi - lo).astype(np.float32)
+        v = np.abs(rng.normal(0, 1e-6, hi - lo)).astype(np.float32)
+        dp, dm, dv = (torch.from_numpy(x.copy()).to(DEV) for x in (p, m, v))
+        hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 4)
+        k3(tab3, gdtype, gdtype, lo, hi, dp, dm, dv, hp, scalars_device(clip_applied=1, coef=0.7))
+        wp, wm, wv = recipe.adamw_step(p, m, v, flat_want[lo:hi], lr=1e-3, betas=(0.9, 0.999),
+                                       eps=1e-8, wd=0.01, step=4, clip_coef=0.7)
+        np.testing.assert_array_equal(dp.cpu().numpy().view(np.int32), wp.view(np.int32))
+        np.testing.assert_array_equal(dm.cpu().numpy().view(np.int32), wm.view(np.int32))
+        np.testing.assert_array_equal(dv.cpu().numpy().view(np.int32), wv.view(np.int32))
+        cast = torch.from_numpy(wp).to(gdtype)
+        for view, off, k in zip(mviews, lay.offsets, sizes):
+            got = view.cpu()
+            a, b = max(off, lo), min(off + k, hi)
+            for i0, i1 in ((off, a), (b, off + k)):           # outside the range: untouched
+                if i1 > i0:
+                    assert bool((got[i0 - off:i1 - off] == 3.0).all())
+            if b > a:
+                np.testing.assert_array_equal(bits(got[a - off:b - off]), bits(cast[a - lo:b - lo]))
+        # K4 over the same range into the same views
+        src = rng.normal(0, 1, hi - lo).astype(np.float32)
+        k4(Table(lay, lo, hi, [None] * len(sizes), mst), gdtype, torch.from_numpy(src).to(DEV), lo, hi)
+        want4 = torch.from_numpy(src).to(gdtype)
+        for view, off, k in zip(mviews, lay.offsets, sizes):
+            a, b = max(off, lo), min(off + k, hi)
+            if b > a:
+                np.testing.assert_array_equal(bits(view.cpu()[a - off:b - off]),
+                                              bits(want4[a - lo:b - lo]))
