@@ -398,3 +398,39 @@ def test_thousands_of_tiny_tensors_against_the_oracle():
         for (off, p), n in zip(g._offsets, g._numels):
             assert torch.equal(p.detach().cpu().view(torch.int16),
                                master[off:off + n].to(torch.float16).view(torch.int16))
+
+
+@pytest.mark.parametrize("stage", [0, 3])
+def test_zero_size_parameter_in_the_list(stage):
+    """An empty parameter among the others changes nothing for them."""
+    from oracle import boundary as ob
+
+    shapes = [(5, 3), (0, 4), (7,), (0,), (33,)]
+    gen = torch.Generator().manual_seed(2)
+    init = [torch.randn(*s, generator=gen) * 0.02 for s in shapes]
+    params = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    module = nn.ParameterList(params)
+    engine = ms.initialize(model=module, model_parameters=list(module),
+                           config=config(dtype="fp16", stage=stage, gas=1, lr=1e-2))
+    ref_params = [nn.Parameter(t.clone()) for t in init]
+    ref = ob.Engine([ref_params], [{"lr": 1e-2, "betas": (0.9, 0.999), "eps": 1e-8,
+                                    "weight_decay": 0.01}], dtype="fp16", zero_stage=stage, clip=1.0,
+                    initial_scale_power=8, loss_scale_window=100,
+                    scheduler_params={"warmup_max_lr": 1e-2})
+    for step in range(3):
+        if stage >= 3:
+            engine.optimizer.gather_parameters()
+            ref.gather_parameters()
+        grads = [(torch.randn(*s, generator=gen) * 256.0 * 1e-2).half() for s in shapes]
+        for p, rp, g in zip(params, ref_params, grads):
+            p.grad = g.to(DEV)
+            rp.grad = g.clone()
+        engine.micro_steps += 1
+        ref.micro_steps += 1
+        assert engine.step() is True and ref.step() is True
+        assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
+        np.testing.assert_allclose(engine.flat_groups[0].data.cpu().numpy(), ref.groups[0].data.numpy(),
+                                   rtol=1e-6, atol=1e-7)
+    if stage >= 3:
+        engine.optimizer.gather_parameters()
+    assert [tuple(p.shape) for p in params] == shapes
