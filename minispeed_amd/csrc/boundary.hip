@@ -682,36 +682,14 @@ __global__ __launch_bounds__(kThreads) void k_accumulate(
 }
 
 // ------------------------------------------------------------- launching
-int cu_count() {
-  static int cached = 0;
-  if (cached == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
-            hipSuccess &&
-        n > 0)
-      cached = n;
-    else
-      cached = 256;
-  }
-  return cached;
-}
-
-// Grid of a streaming kernel: `blocks_per_cu` resident blocks per CU that
-// walk the tiles grid-stride, or (blocks_per_cu <= 0) one block per tile.
-int stream_grid(int64_t ntiles, int blocks_per_cu) {
-  int64_t g = blocks_per_cu > 0 ? static_cast<int64_t>(cu_count()) * blocks_per_cu
-                                : ntiles;
-  if (g > ntiles) g = ntiles;
+// Grid of a streaming kernel: one block per tile.  The kernels also walk
+// their tiles grid-stride, so a clamped grid (more than 2^31 - 1 tiles)
+// still covers every tile.
+int stream_grid(int64_t ntiles) {
+  int64_t g = ntiles;
   if (g > 0x7fffffff) g = 0x7fffffff;
   if (g < 1) g = 1;
   return static_cast<int>(g);
-}
-
-int env_int(const char* name, int fallback) {
-  const char* s = getenv(name);
-  if (!s || !*s) return fallback;
-  return atoi(s);
 }
 
 int launch_status() {
@@ -776,7 +754,7 @@ void launch_adamw(float* p, float* m, float* v, const float* fg,
                   const AdamScalars& h, const ms_step_scalars_t* sc,
                   hipStream_t st) {
   const int64_t ntiles = (end - begin + kTile - 1) / kTile;
-  const dim3 grid(stream_grid(ntiles, env_int("MS_ADAMW_BLOCKS_PER_CU", 0)));
+  const dim3 grid(stream_grid(ntiles));
   const dim3 block(kThreads);
   if (fg)
     hipLaunchKernelGGL((k_adamw<G, M, true>), grid, block, 0, st, p, m, v, fg,
@@ -926,7 +904,7 @@ int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n
   if (n == 0) return MS_OK;
   if (!dst || !src) return MS_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(stream_grid((n + kTile - 1) / kTile, 0));
+  const dim3 grid(stream_grid((n + kTile - 1) / kTile));
   const dim3 block(kThreads);
   const int f = first ? 1 : 0;
   switch (src_dtype) {
@@ -952,7 +930,7 @@ int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
   if (!segs || nseg <= 0 || nseg > kMaxSegs) return MS_ETABLE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t ntiles = (end - begin + kCastTile - 1) / kCastTile;
-  const dim3 grid(stream_grid(ntiles, env_int("MS_CAST_BLOCKS_PER_CU", 0)));
+  const dim3 grid(stream_grid(ntiles));
   const dim3 block(kCastThreads);
   switch (model_dtype) {
     case MS_DTYPE_F32:
