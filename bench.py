@@ -68,6 +68,8 @@ def parse(argv=None):
     ap.add_argument("--mode", default="fused", choices=["fused", "materialize", "contiguous"])
     ap.add_argument("--zero-stage", type=int, default=1, choices=[0, 1, 2, 3],
                     help="ZeRO stage at world size 1 (3: also times the parameter gather)")
+    ap.add_argument("--state-spacing-gib", type=float, default=32.0,
+                    help="hip_boundary.state_spacing_gib of the engine (0: masters and moments packed)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without the per-kernel HIP events (no roofline)")
@@ -78,7 +80,7 @@ def parse(argv=None):
     return ap.parse_args(argv)
 
 
-def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1) -> dict:
+def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1, state_spacing_gib: float = 32.0) -> dict:
     cfg = {
         "train_micro_batch_size_per_gpu": 1,
         "gradient_accumulation_steps": 1,
@@ -91,7 +93,8 @@ def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1) -> dict:
                                  "warmup_num_steps": 100, "total_num_steps": 1000}},
         "zero_optimization": {"stage": zero_stage},
         "hip_boundary": {"materialize_flat_grad": mode == "materialize",
-                         "contiguous_gradients": mode == "contiguous"},
+                         "contiguous_gradients": mode == "contiguous",
+                         "state_spacing_gib": state_spacing_gib},
         "steps_per_print": 1000000,
     }
     if grad_dtype == "fp16":
@@ -189,7 +192,7 @@ def bench_llama_shard(args) -> dict:
 
     from minispeed_amd import _native
     from minispeed_amd.boundary import LaunchTimer, adamw_params
-    from minispeed_amd.flat import FlatLayout, check_table
+    from minispeed_amd.flat import STATE_SPACING_BYTES, FlatLayout, check_table, spaced_buffers
     from minispeed_amd.workloads import shapes_of
 
     lib = _native.load()
@@ -202,11 +205,15 @@ def bench_llama_shard(args) -> dict:
     S, N = hi - lo, lay.numel_padded
     log(f"[bench] llama3-8b: {len(shapes)} tensors, {N:,} params; rank 3 of 8 owns [{lo:,}, {hi:,})")
     gen = torch.Generator(device=dev).manual_seed(5)
-    grad = (torch.randn(S, generator=gen, device=dev) * 1e-4).to(torch.bfloat16)
+    # the partitioned masters and the moments, placed as the engine places
+    # them with hip_boundary.state_spacing_gib = 32
+    master, m, v = spaced_buffers([S, S, S], dev, STATE_SPACING_BYTES)
+    master.normal_(0.0, 0.02, generator=gen)
+    grad = torch.empty(S, dtype=torch.bfloat16, device=dev)
+    for a in range(0, S, 1 << 27):   # bounded fp32 temporaries
+        b = min(S, a + (1 << 27))
+        grad[a:b] = torch.randn(b - a, generator=gen, device=dev) * 1e-4
     holder = torch.empty(S, dtype=torch.bfloat16, device=dev)
-    master = torch.randn(S, generator=gen, device=dev) * 0.02
-    m = torch.zeros(S, device=dev)
-    v = torch.zeros(S, device=dev)
     gs, ms_ = [], []
     for off, n in zip(lay.offsets, numels):
         a, b = max(off, lo), min(off + n, hi)
@@ -355,7 +362,8 @@ def main(argv=None) -> int:
     params = [nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
     module = nn.ParameterList(params)
     engine = ms.initialize(model=module, model_parameters=list(module),
-                           config=engine_config(args.grad_dtype, args.mode, args.zero_stage))
+                           config=engine_config(args.grad_dtype, args.mode, args.zero_stage,
+                                                args.state_spacing_gib))
     mult = 2.0 ** 16 if args.grad_dtype == "fp16" else 1.0
     grad_sets = []
     for _ in range(2):
@@ -463,6 +471,7 @@ def main(argv=None) -> int:
             "zero_stage": args.zero_stage,
             "world_size": 1,
             "mode": args.mode,
+            "state_spacing_gib": args.state_spacing_gib,
             "clip": 1.0,
             "bytes_per_param": b1 + b3,
         },

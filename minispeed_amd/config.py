@@ -15,7 +15,8 @@ minispeed config drives this package unchanged:
 
 One section is specific to this package and ignored by minispeed:
 
-    "hip_boundary": {"materialize_flat_grad": false, "contiguous_gradients": false}
+    "hip_boundary": {"materialize_flat_grad": false, "contiguous_gradients": false,
+                     "state_spacing_gib": 0}
 
 With ``materialize_flat_grad`` the ragged-grad kernel also writes the fp32
 flat gradient buffer and the AdamW kernel reads it back (36 B/param for half
@@ -27,6 +28,13 @@ fp32 straight into a flat buffer as backward produces it, instead of in the
 parameter dtype in ``param.grad``; ``param.grad`` is released after each
 backward.  This changes the numerics (fp32 instead of half accumulation), so
 it is not bitwise minispeed and is off by default.
+
+``state_spacing_gib`` (opt-in, 0 = off) puts each group's fp32 masters,
+exp_avg and exp_avg_sq in one allocation, each at least that many GiB after
+the previous one.  On MI355X 32 makes the fused AdamW kernel about 10%
+faster at the price of the gaps (about 54 GiB of HBM for a 1.3B-param
+group; nothing once each buffer is 32 GiB or larger).  The placement
+changes no result.
 """
 
 from __future__ import annotations
@@ -83,6 +91,11 @@ class DeepSpeedConfig:
         hip = _section(raw, "hip_boundary")
         self.materialize_flat_grad = bool(hip.get("materialize_flat_grad", False))
         self.contiguous_gradients = bool(hip.get("contiguous_gradients", False))
+        spacing = hip.get("state_spacing_gib", 0)
+        if spacing is None or isinstance(spacing, bool) or not isinstance(spacing, (int, float)) \
+                or spacing < 0:
+            raise ConfigError(f"hip_boundary.state_spacing_gib must be a number >= 0, got {spacing!r}")
+        self.state_spacing_bytes = int(float(spacing) * (1 << 30))
 
     # ------------------------------------------------------------ sections
     def _parse_batch(self, raw: dict, world: int) -> None:

@@ -91,6 +91,7 @@ class DeepSpeedEngine:
         self.flat_groups, option_groups = build_flat_groups(
             groups, rank=self.rank, world_size=self.world_size,
             zero_stage=self.config.zero_stage, device=self.device,
+            state_spacing=self.config.state_spacing_bytes,
         )
         for g in self.flat_groups:
             g.copy_model_to_flat()

@@ -34,11 +34,10 @@ class FlatAdam:
                 group.setdefault(key, value)
             self.param_groups.append(group)
             n = flat.numel_shard()
-            self._state.append({
-                "step": 0,
-                "exp_avg": torch.zeros(n, dtype=torch.float32, device=flat.device),
-                "exp_avg_sq": torch.zeros(n, dtype=torch.float32, device=flat.device),
-            })
+            moments = flat.take_moment_buffers()
+            if moments is None or any(t.numel() != n for t in moments):
+                moments = tuple(torch.zeros(n, dtype=torch.float32, device=flat.device) for _ in range(2))
+            self._state.append({"step": 0, "exp_avg": moments[0], "exp_avg_sq": moments[1]})
         self._clean = None  # device "no overflow, no clip" scalars for step()
 
     @staticmethod

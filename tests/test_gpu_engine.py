@@ -434,3 +434,67 @@ def test_zero_size_parameter_in_the_list(stage):
     if stage >= 3:
         engine.optimizer.gather_parameters()
     assert [tuple(p.shape) for p in params] == shapes
+
+
+def test_spaced_state_buffers_are_views_of_one_arena():
+    """With a spacing the buffers are zeroed views of one allocation, each
+    starting max(spacing, previous size) bytes (rounded up to 2 MiB) after the
+    previous one; without, separate allocations."""
+    from minispeed_amd.flat import spaced_buffers
+
+    dev = torch.device(DEV)
+    mib = 1 << 20
+    n = 3 * mib + 5                 # 12 MiB + 20 bytes: larger than the spacing below
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(dev)
+    bufs = spaced_buffers([1000, n, 1000], dev, 8 * mib)
+    torch.cuda.synchronize()
+    assert [b.numel() for b in bufs] == [1000, n, 1000]
+    assert all(b.dtype == torch.float32 and b.is_contiguous() and int(b.count_nonzero()) == 0 for b in bufs)
+    base = bufs[0].untyped_storage().data_ptr()
+    assert all(b.untyped_storage().data_ptr() == base for b in bufs)
+    assert bufs[1].data_ptr() - bufs[0].data_ptr() == 8 * mib
+    assert bufs[2].data_ptr() - bufs[1].data_ptr() == 14 * mib      # 4n rounded up to 2 MiB
+    assert torch.cuda.memory_allocated(dev) - before >= 22 * mib + 4000
+    bufs[1].fill_(1.0)
+    assert int(bufs[0].count_nonzero()) == 0 and int(bufs[2].count_nonzero()) == 0
+    plain = spaced_buffers([1000, 1000, 1000], dev, 0)
+    assert len({b.untyped_storage().data_ptr() for b in plain}) == 3
+
+
+@pytest.mark.parametrize("stage", [1, 3])
+def test_state_spacing_changes_no_result(stage):
+    """The same steps with the masters and moments in a spaced arena and in
+    separate allocations give bitwise the same masters, moments and model."""
+    runs = []
+    for spacing in (0, 0.01):
+        torch.manual_seed(0)
+        module = nn.Sequential(nn.Linear(96, 64), nn.GELU(), nn.Linear(64, 8)).to(DEV)
+        cfg = config(dtype="fp16", stage=stage, gas=1)
+        cfg["hip_boundary"] = {"state_spacing_gib": spacing}
+        engine = ms.initialize(model=module, model_parameters=list(module.parameters()), config=cfg)
+        gen = torch.Generator().manual_seed(1)
+        for _ in range(3):
+            if stage >= 3:
+                engine.optimizer.gather_parameters()
+            x = torch.randn(16, 96, generator=gen).to(DEV).half()
+            loss = engine(x).float().pow(2).mean()
+            engine.backward(loss)
+            engine.step()
+        if stage >= 3:
+            engine.optimizer.gather_parameters()
+        st = engine.optimizer.state[0]
+        runs.append([engine.flat_groups[0].data.clone(), st["exp_avg"].clone(), st["exp_avg_sq"].clone()]
+                    + [p.detach().clone() for p in module.parameters()])
+    for a, b in zip(*runs):
+        assert torch.equal(a.view(torch.int8), b.view(torch.int8))
+
+
+def test_engine_takes_the_moments_allocated_with_the_masters():
+    module = nn.Linear(64, 32).to(DEV)
+    engine = ms.initialize(model=module, model_parameters=list(module.parameters()),
+                           config=config(dtype="bf16", stage=1, gas=1))
+    g = engine.flat_groups[0]
+    assert g.take_moment_buffers() is None            # handed to the optimizer
+    st = engine.optimizer.state[0]
+    assert st["exp_avg"].numel() == st["exp_avg_sq"].numel() == g.numel_shard()
