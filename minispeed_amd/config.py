@@ -34,7 +34,9 @@ exp_avg and exp_avg_sq in one allocation, each at least that many GiB after
 the previous one.  On MI355X 32 makes the fused AdamW kernel about 10%
 faster at the price of the gaps (about 54 GiB of HBM for a 1.3B-param
 group; nothing once each buffer is 32 GiB or larger).  The placement
-changes no result.
+changes no result.  The three tensors are then views of one allocation:
+``torch.save`` them through ``state_dict()`` / the checkpoint functions
+(which copy them out), not directly.
 """
 
 from __future__ import annotations
