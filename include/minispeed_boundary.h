@@ -29,13 +29,23 @@
 extern "C" {
 #endif
 
-#define MS_ABI_VERSION 2
+#define MS_ABI_VERSION 3
 
 /* element types of ragged gradient / model storage */
 enum {
   MS_DTYPE_F32 = 0,
   MS_DTYPE_F16 = 1,
   MS_DTYPE_BF16 = 2
+};
+
+/* what ms_grad_stats does to each widened gradient with `grad_scale`
+ * (ms_fused_adamw accepts NONE and DIVIDE) */
+enum {
+  MS_SCALE_NONE = 0,      /* g                                           */
+  MS_SCALE_DIVIDE = 1,    /* g / grad_scale, IEEE (unscale_grads,
+                             flat.py:243-247); grad_scale > 0            */
+  MS_SCALE_MULTIPLY = 2   /* g * grad_scale, one rounding (scale_grads,
+                             flat.py:249-257)                            */
 };
 
 /* host-side argument errors (nothing launched) */
@@ -108,7 +118,8 @@ typedef struct ms_adamw_params {
   float eps;             /* fp32(eps)                  add_               */
   float grad_scale;      /* loss scale to divide ragged grads by          */
   int32_t decay;         /* weight_decay != 0 (adam.py:81)                */
-  int32_t unscale;       /* divide ragged grads by grad_scale (flat.py:247)*/
+  int32_t unscale;       /* MS_SCALE_DIVIDE: divide ragged grads by
+                            grad_scale (flat.py:247); or MS_SCALE_NONE   */
 } ms_adamw_params_t;
 
 /* MS_ABI_VERSION of the loaded library. */
@@ -126,21 +137,26 @@ int ms_stats_blocks(void);
 /*
  * K1 — ragged gradient scan.  Replaces FlatParamGroup.flatten_grads
  * (flat.py:196-213), has_overflow on the flat grad (precision.py:79-87),
- * unscale_grads (flat.py:243-247) and local_grad_sumsq (flat.py:232-234).
+ * unscale_grads (flat.py:243-247), scale_grads (flat.py:249-257) and
+ * local_grad_sumsq (flat.py:232-234).
  *
  * Scans flat indices [begin, end) through `segs` [dev] (`nseg` entries,
  * grad dtype `grad_dtype`):
  *   - overflow: block_flag[b] != 0 iff some grad element handled by block b
  *     is inf/nan, tested on the raw stored value (before unscale);
- *   - g = fp32(grad) / grad_scale when `unscale` (IEEE division), else the
- *     exact widening fp32(grad);
+ *   - g = the exact widening fp32(grad), then per `unscale`
+ *     (MS_SCALE_*): unchanged, / grad_scale (IEEE division) or
+ *     * grad_scale (one rounded multiply);
  *   - flat_grad [dev, optional]: flat_grad[i - begin] = g for every i;
  *   - block_sumsq [dev, optional]: per-block fp64 sum of g*g over the owned
  *     range [own_begin, own_end); with block_flag [dev] it must hold
  *     nblk >= ms_stats_blocks() slots, and all nblk slots are written
  *     (zeros after the last block's).
  * With block_sumsq == NULL and block_flag == NULL the call is a pure ragged
- * flatten (FlatParamGroup.copy_model_to_flat, flat.py:115-131).
+ * flatten (FlatParamGroup.copy_model_to_flat, flat.py:115-131).  flat_grad
+ * may be the storage of a single F32 segment spanning [begin, end): each
+ * element is read before it is written, by the same lane, so the call then
+ * scales the buffer in place (unscale_grads / scale_grads).
  */
 int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
                   int64_t begin, int64_t end, int64_t own_begin,

@@ -19,11 +19,15 @@ from typing import Optional
 import torch  # noqa: F401  (must precede the dlopen below, see module doc)
 
 LIB_NAME = "libminispeed_boundary.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
+
+SCALE_NONE = 0
+SCALE_DIVIDE = 1
+SCALE_MULTIPLY = 2
 
 _TORCH_TO_MS = {
     torch.float32: DTYPE_F32,

@@ -280,6 +280,52 @@ def run_boundary(
 
 
 # ------------------------------------------------------------------ utility
+def _whole_buffer_table(flat: torch.Tensor) -> torch.Tensor:
+    """Device segment table of one row covering a contiguous buffer."""
+    table = np.array([[0, flat.numel(), flat.data_ptr(), 0]], dtype=np.int64)
+    return torch.from_numpy(table).to(flat.device)
+
+
+def scale_in_place(buf: torch.Tensor, mode: int, factor: float) -> None:
+    """``buf.div_(factor)`` (mode SCALE_DIVIDE, flat.py:243-247) or
+    ``buf.mul_(factor)`` (mode SCALE_MULTIPLY, flat.py:249-257) of a
+    contiguous fp32 device buffer, in place by K1, with ``factor`` rounded to
+    fp32 first as torch does with a Python scalar."""
+    _native.require_hip_tensor(buf, "scaled buffer")
+    if buf.dtype != torch.float32 or not buf.is_contiguous():
+        raise TypeError("scale_in_place needs a contiguous float32 buffer")
+    n = buf.numel()
+    if n == 0:
+        return
+    table = _whole_buffer_table(buf)
+    _native.check(_native.load().ms_grad_stats(
+        table.data_ptr(), 1, _native.DTYPE_F32, 0, n, 0, 0, mode, float(np.float32(factor)),
+        buf.data_ptr(), None, None, 0, _native.stream_handle(buf.device)), "ms_grad_stats(scale)")
+
+
+def sumsq_device(buf: torch.Tensor) -> torch.Tensor:
+    """``buf.pow(2).sum()`` as a 0-dim fp32 device tensor (flat.py:232-234):
+    K1's fp64 per-block partials summed by K2 and rounded to fp32 once."""
+    _native.require_hip_tensor(buf, "sum-of-squares buffer")
+    flat = buf.detach().reshape(-1)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    n = flat.numel()
+    if n == 0:
+        return torch.zeros((), dtype=torch.float32, device=flat.device)
+    lib = _native.load()
+    ws = Workspace(flat.device, 1)
+    table = _whole_buffer_table(flat)
+    stream = _native.stream_handle(flat.device)
+    psum, pflag = ws.partial_ptrs(0)
+    _native.check(lib.ms_grad_stats(table.data_ptr(), 1, _native.ms_dtype(flat.dtype), 0, n, 0, n, 0,
+                                    1.0, None, psum, pflag, ws.nblk, stream), "ms_grad_stats")
+    _native.check(lib.ms_norm_clip(psum, pflag, ws.nblk, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0,
+                                   ws.scalars.data_ptr(), None, stream), "ms_norm_clip")
+    off = _native.StepScalars.sumsq.offset
+    return ws.scalars[off:off + 4].view(torch.float32).clone().reshape(())
+
+
 def scan_nonfinite(buf: torch.Tensor) -> bool:
     """inf/nan test of one device buffer with K1 + K2 (used by
     precision.has_overflow)."""
@@ -291,8 +337,7 @@ def scan_nonfinite(buf: torch.Tensor) -> bool:
     dtype = _native.ms_dtype(flat.dtype)
     lib = _native.load()
     ws = Workspace(flat.device, 1)
-    table = np.array([[0, n, flat.data_ptr(), 0]], dtype=np.int64)
-    dev_table = torch.from_numpy(table).to(flat.device)
+    dev_table = _whole_buffer_table(flat)
     stream = _native.stream_handle(flat.device)
     psum, pflag = ws.partial_ptrs(0)
     _native.check(lib.ms_grad_stats(dev_table.data_ptr(), 1, dtype, 0, n, 0, 0, 0, 1.0,

@@ -237,10 +237,12 @@ __device__ inline int64_t seg_end(const ms_segment_t& s) {
 
 // Loss-scale division.  mode 0: none; 1: multiply by the exact reciprocal of
 // a power-of-two scale (x / 2^k and x * 2^-k round identically, subnormal
-// results included); 2: IEEE division.
+// results included); 2: IEEE division; 3: one rounded multiply by `scale`
+// (the clip coefficient of scale_grads, flat.py:249-257).
 __device__ inline float unscale1(float g, int mode, float scale, float inv) {
   if (mode == 1) return g * inv;
   if (mode == 2) return g / scale;
+  if (mode == 3) return g * scale;
   return g;
 }
 
@@ -697,10 +699,12 @@ int launch_status() {
   return e == hipSuccess ? MS_OK : static_cast<int>(e);
 }
 
-// How a kernel divides by the loss scale (see unscale1).
+// How a kernel divides by the loss scale (see unscale1).  `unscale` is
+// MS_SCALE_NONE, MS_SCALE_DIVIDE or MS_SCALE_MULTIPLY (checked by the caller).
 int unscale_mode(int32_t unscale, float scale, float* inv) {
   *inv = 1.0f;
-  if (!unscale) return 0;
+  if (unscale == MS_SCALE_NONE) return 0;
+  if (unscale == MS_SCALE_MULTIPLY) return 3;
   int e = 0;
   const float mant = frexpf(scale, &e);   // scale = mant * 2^e
   if (mant == 0.5f && e - 1 <= 126 && e - 1 >= -126) {
@@ -819,7 +823,9 @@ int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
   if (block_sumsq != nullptr && nblk < kStatsBlocks) return MS_EBLOCKS;
   if (end > begin && (segs == nullptr || nseg <= 0)) return MS_ETABLE;
   if (nseg < 0 || nseg > kMaxSegs) return MS_ETABLE;
-  if (unscale && !(grad_scale > 0.0f)) return MS_EINVAL;
+  if (unscale != MS_SCALE_NONE && unscale != MS_SCALE_DIVIDE && unscale != MS_SCALE_MULTIPLY)
+    return MS_EINVAL;
+  if (unscale == MS_SCALE_DIVIDE && !(grad_scale > 0.0f)) return MS_EINVAL;
   if (block_sumsq == nullptr && end == begin) return MS_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (grad_dtype) {
@@ -866,7 +872,8 @@ int ms_fused_adamw(float* master, float* exp_avg, float* exp_avg_sq,
   if (end == begin) return MS_OK;
   if (!master || !exp_avg || !exp_avg_sq) return MS_EINVAL;
   if (!segs || nseg <= 0 || nseg > kMaxSegs) return MS_ETABLE;
-  if (hp->unscale && !(hp->grad_scale > 0.0f)) return MS_EINVAL;
+  if (hp->unscale != MS_SCALE_NONE && hp->unscale != MS_SCALE_DIVIDE) return MS_EINVAL;
+  if (hp->unscale == MS_SCALE_DIVIDE && !(hp->grad_scale > 0.0f)) return MS_EINVAL;
   AdamScalars h;
   h.neg_lr = hp->neg_lr;
   h.decay_alpha = hp->decay_alpha;

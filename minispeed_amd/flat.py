@@ -722,6 +722,37 @@ class FlatParamGroup:
             return self.grad_shard
         return self.grad[self.shard_start:self.shard_end]
 
+    # The unfused step pieces of the reference (flat.py:232-257).  The fused
+    # boundary does all three inside K1-K3 without a flat gradient; these
+    # work on the materialized ``grad`` / ``grad_shard`` (after
+    # ``flatten_grads``) for callers that drive the steps one by one.
+    def local_grad_sumsq(self) -> torch.Tensor:
+        """Sum of squares of the owned gradient slice, a 0-dim fp32 device
+        tensor (flat.py:232-234)."""
+        from .boundary import sumsq_device
+        return sumsq_device(self.grad_for_shard())
+
+    @torch.no_grad()
+    def unscale_grads(self, scale: float) -> None:
+        """``grad /= scale`` over the whole flat gradient (flat.py:243-247)."""
+        if scale == 1.0 or self.grad is None:
+            return
+        from .boundary import scale_in_place
+        scale_in_place(self.grad, _native.SCALE_DIVIDE, scale)
+
+    @torch.no_grad()
+    def scale_grads(self, factor: float) -> None:
+        """Multiply the owned gradients by a clip coefficient
+        (flat.py:249-257): ``grad_shard`` if it exists, else ``grad``."""
+        if factor == 1.0:
+            return
+        target = self.grad_shard if self.grad_shard is not None else self.grad
+        if target is None:
+            return
+        from .boundary import scale_in_place
+        scale_in_place(target, _native.SCALE_MULTIPLY, factor)
+        self._grad_dirty = True
+
     @property
     def shard(self) -> torch.Tensor:
         if self._partitioned:

@@ -69,6 +69,35 @@ class ZeROOptimizer:
         for g in self.flat_groups:
             g.copy_flat_to_model()
 
+    # ----------------------------------------- unfused step pieces (W = 1)
+    @torch.no_grad()
+    def reduce_gradients(self) -> None:
+        """stage_1_and_2.py:86-102 at world size 1: stages 0/1 leave the
+        flat gradient as it is (an all-reduce over one rank, no division),
+        stage 2 copies it into ``grad_shard`` (the one-rank reduce-scatter)."""
+        for g in self.flat_groups:
+            if self.zero_stage >= 2:
+                comm.reduce_scatter(g.grad_shard, g.grad)
+            else:
+                comm.all_reduce(g.grad)
+
+    @torch.no_grad()
+    def clip_gradients(self, max_norm: Optional[float]) -> float:
+        """stage_1_and_2.py:105-128: the global L2 norm of the owned
+        gradients (group sums of squares added in fp32, fp32 sqrt), and, if
+        ``max_norm`` is set and the norm exceeds it, every group's owned
+        gradients multiplied by ``max_norm / (norm + 1e-6)``."""
+        total = torch.zeros((), dtype=torch.float32, device=self.flat_groups[0].device)
+        for g in self.flat_groups:
+            total += g.local_grad_sumsq()
+        norm = float(total.sqrt().item())
+        self.grad_norm = norm
+        if max_norm is not None and norm > max_norm:
+            coef = max_norm / (norm + 1e-6)
+            for g in self.flat_groups:
+                g.scale_grads(coef)
+        return norm
+
     @torch.no_grad()
     def step(self) -> bool:
         """Unfused AdamW over already reduced/clipped grads (the reference's

@@ -74,6 +74,14 @@ class ZeROStage3Optimizer(ZeROOptimizer):
         return True
 
     # ------------------------------------------------------ fused boundary
+    @torch.no_grad()
+    def reduce_gradients(self) -> None:
+        """stage_3.py:120-126: the one-rank reduce-scatter into
+        ``grad_shard``, then the full flat gradient is dropped."""
+        super().reduce_gradients()
+        for g in self.flat_groups:
+            g.grad = None
+
     def _model_targets(self) -> List[Optional[List[int]]]:
         if not self._gathered:
             # the reference's free_parameters is a no-op then: nothing written

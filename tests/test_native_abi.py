@@ -101,6 +101,13 @@ def test_host_argument_errors_return_codes_without_launching():
     hp.unscale = 1
     hp.grad_scale = 0.0
     assert lib.ms_fused_adamw(8, 8, 8, None, 8, 1, 1, 1, 0, 10, ctypes.byref(hp), 8, None) == EINVAL
+    hp.unscale = _native.SCALE_MULTIPLY           # K3 only divides
+    hp.grad_scale = 2.0
+    assert lib.ms_fused_adamw(8, 8, 8, None, 8, 1, 1, 1, 0, 10, ctypes.byref(hp), 8, None) == EINVAL
+    # K1: scaling mode out of range; divide by a non-positive scale
+    assert lib.ms_grad_stats(8, 1, 0, 0, 10, 0, 0, 3, 1.0, 8, None, None, 0, None) == EINVAL
+    assert lib.ms_grad_stats(8, 1, 0, 0, 10, 0, 0, _native.SCALE_DIVIDE, -1.0, 8, None, None, 0,
+                             None) == EINVAL
     assert lib.ms_cast_to_model(None, 0, 10, 8, 1, 1, None) == EINVAL
     assert lib.ms_cast_to_model(8, 0, 10, None, 0, 1, None) == ETABLE
     assert lib.ms_cast_to_model(8, 0, 10, 8, 1, 5, None) == EINVAL
@@ -109,6 +116,15 @@ def test_host_argument_errors_return_codes_without_launching():
         assert lib.ms_error_string(code)
     with pytest.raises(RuntimeError, match="segment count"):
         _native.check(ETABLE, "probe")
+
+
+def test_header_constants_match_the_binding():
+    with open(HEADER) as f:
+        text = f.read()
+    consts = {k: int(v) for k, v in re.findall(r"\b(MS_[A-Z0-9_]+)\s*=\s*(-?\d+)", text)}
+    assert int(re.search(r"#define MS_ABI_VERSION (\d+)", text).group(1)) == _native.ABI_VERSION
+    for name in ("DTYPE_F32", "DTYPE_F16", "DTYPE_BF16", "SCALE_NONE", "SCALE_DIVIDE", "SCALE_MULTIPLY"):
+        assert consts["MS_" + name] == getattr(_native, name), name
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
