@@ -192,7 +192,7 @@ def bench_llama_shard(args) -> dict:
 
     from minispeed_amd import _native
     from minispeed_amd.boundary import LaunchTimer, adamw_params
-    from minispeed_amd.flat import STATE_SPACING_BYTES, FlatLayout, check_table, spaced_buffers
+    from minispeed_amd.flat import STATE_SPACING_BYTES, FlatLayout, check_table, state_buffers
     from minispeed_amd.workloads import shapes_of
 
     lib = _native.load()
@@ -207,7 +207,7 @@ def bench_llama_shard(args) -> dict:
     gen = torch.Generator(device=dev).manual_seed(5)
     # the partitioned masters and the moments, placed as the engine places
     # them with hip_boundary.state_spacing_gib = 32
-    master, m, v = spaced_buffers([S, S, S], dev, STATE_SPACING_BYTES)
+    master, m, v = state_buffers([[S, S, S]], dev, STATE_SPACING_BYTES)[0]
     master.normal_(0.0, 0.02, generator=gen)
     grad = torch.empty(S, dtype=torch.bfloat16, device=dev)
     for a in range(0, S, 1 << 27):   # bounded fp32 temporaries

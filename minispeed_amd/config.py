@@ -29,14 +29,14 @@ parameter dtype in ``param.grad``; ``param.grad`` is released after each
 backward.  This changes the numerics (fp32 instead of half accumulation), so
 it is not bitwise minispeed and is off by default.
 
-``state_spacing_gib`` (opt-in, 0 = off) puts each group's fp32 masters,
-exp_avg and exp_avg_sq in one allocation, each at least that many GiB after
-the previous one.  On MI355X 32 makes the fused AdamW kernel about 10%
-faster at the price of the gaps (about 54 GiB of HBM for a 1.3B-param
-group; nothing once each buffer is 32 GiB or larger).  The placement
-changes no result.  The three tensors are then views of one allocation:
-``torch.save`` them through ``state_dict()`` / the checkpoint functions
-(which copy them out), not directly.
+``state_spacing_gib`` (opt-in, 0 = off) puts the fp32 masters, exp_avg and
+exp_avg_sq of all groups in one allocation of three windows of that many
+GiB, one window per array.  On MI355X 32 makes the fused AdamW kernel about
+10% faster at the price of the unused part of the windows (96 GiB in all:
+about 80 GiB more than the state of a 1.3B-param model, about 6 GiB more at
+8B).  The placement changes no result.  The tensors are then views of one
+allocation: ``torch.save`` them through ``state_dict()`` / the checkpoint
+functions (which copy them out), not directly.
 """
 
 from __future__ import annotations

@@ -14,7 +14,7 @@ Device buffers, all fp32 and resident in HBM (flat.py:61-73):
                   the boundary)
   ``grad_shard``  owned gradient slice, stage >= 2
 and the AdamW moments of the owned range, allocated with the masters so the
-three can be placed apart in HBM (``spaced_buffers``) and handed to the
+three can be placed apart in HBM (``state_buffers``) and handed to the
 optimizer (``take_moment_buffers``).
 
 The boundary kernels address ragged per-parameter storage (``param.grad``,
@@ -238,8 +238,8 @@ def _flat_view(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
-# Distance between the starts of the masters, exp_avg and exp_avg_sq that
-# ``hip_boundary.state_spacing_gib`` asks for when it is turned on.
+# Window of the state arena that ``hip_boundary.state_spacing_gib`` asks for
+# when it is turned on (32 GiB).
 STATE_SPACING_BYTES = 32 << 30
 _ARENA_SLACK_BYTES = 1 << 30
 _ARENA_ALIGN = 1 << 21
@@ -247,45 +247,76 @@ _ARENA_ALIGN = 1 << 21
 _log = logging.getLogger("minispeed_amd")
 
 
-def spaced_buffers(numels: Sequence[int], device: torch.device, spacing: int) -> List[torch.Tensor]:
-    """Zeroed fp32 buffers of the given sizes: with ``spacing`` > 0, views of
-    one allocation (an arena) in which buffer k starts at least ``spacing``
-    bytes after buffer k-1; with ``spacing`` 0, separate allocations.
+def state_sizes(layout: "FlatLayout", zero_stage: int) -> Tuple[int, int, int]:
+    """Element counts of a group's (masters, exp_avg, exp_avg_sq): the
+    masters cover the whole padded space, or only the owned shard when a
+    ZeRO-3 partition will shrink them to it; the moments cover the owned
+    range (optim/adam.py:38-56)."""
+    n_own = layout.shard_end - layout.shard_start
+    if zero_stage >= 3 and n_own != layout.numel_padded:
+        return n_own, n_own, n_own
+    return layout.numel_padded, n_own, n_own
 
-    The fused AdamW kernel reads and writes the masters, exp_avg and
-    exp_avg_sq at the same flat index in lockstep.  On MI355X that streams
-    faster when the three are far apart in *physical* HBM: at 1.3B params
-    the kernel takes 5.87-5.89 ms with the three 32 GiB apart inside one
-    allocation, against 6.5-6.7 ms for three separate allocations (whose
+
+def state_buffers(sizes: Sequence[Sequence[int]], device: torch.device,
+                  window: int) -> List[List[torch.Tensor]]:
+    """Zeroed fp32 buffers, ``sizes[g][j]`` elements for array j of group g.
+
+    With ``window`` 0 they are separate allocations.  With a window they are
+    views of one allocation (the state arena) of ``k`` windows of ``window``
+    bytes: array j of every group lies in window j, the groups back to back
+    at the same offsets in every window.  The fused AdamW kernel reads and
+    writes the masters, exp_avg and exp_avg_sq at the same flat index in
+    lockstep, and on MI355X that streams faster when the three are at least
+    ~32 GiB apart in *physical* HBM: 1.3B params, 5.87-5.93 ms with the
+    three 32 GiB apart against 6.0-6.7 ms in separate allocations (whose
     physical placement varies from process to process) and 6.8 ms packed
     back to back.  Mapping the same physical chunks at packed or spaced
     virtual addresses (and the reverse) shows that only the physical
-    distance counts, and only one allocation keeps the distance between its
-    parts fixed, so the gaps stay allocated: the arena holds
-    ``2 * spacing + size`` bytes when the buffers are smaller than
-    ``spacing`` (about 54 GiB more than the buffers at 1.3B params) and no
-    more than the buffers once each is at least ``spacing`` bytes.  Falls
-    back to separate allocations (with a log line) when the device does not
-    have the free memory.  The placement changes no result.
+    distance counts.  A whole window per array is what keeps the distance
+    in every allocator state: the driver builds an allocation from
+    naturally aligned power-of-two physical blocks, so arrays at multiples
+    of 32 GiB in an allocation of whole 32 GiB windows stay 32 GiB (or a
+    multiple) apart, while a tighter arena puts the last array in a smaller
+    block anywhere in memory.  The arena therefore holds ``k * window``
+    bytes (96 GiB at 32 GiB: about 80 GiB more than the state of a
+    1.3B-param group, about 6 GiB more at 8B).  Columns larger than a window
+    are allocated separately (arrays that large lie far apart anyway), and
+    so is everything when the device lacks the free memory (with a log
+    line).  The placement changes no result.
     """
-    def plain() -> List[torch.Tensor]:
-        return [torch.zeros(n, dtype=torch.float32, device=device) for n in numels]
+    def plain() -> List[List[torch.Tensor]]:
+        return [[torch.zeros(int(n), dtype=torch.float32, device=device) for n in row] for row in sizes]
 
-    if spacing <= 0 or len(numels) < 2:
+    if window <= 0 or not sizes:
         return plain()
-    offsets, pos = [], 0
-    for k, n in enumerate(numels):
-        offsets.append(pos)
-        step = 4 * int(n) if k == len(numels) - 1 else max(spacing, 4 * int(n))
-        pos += -(-step // _ARENA_ALIGN) * _ARENA_ALIGN
-    total = offsets[-1] + 4 * int(numels[-1])
+    k = len(sizes[0])
+    if any(len(row) != k for row in sizes):
+        raise ValueError("every group needs the same number of state arrays")
+    window = _round_up(int(window), _ARENA_ALIGN)
+    fill = [0] * k
+    offsets = []
+    for row in sizes:
+        offsets.append(list(fill))
+        for j, n in enumerate(row):
+            fill[j] += _round_up(4 * int(n), _ARENA_ALIGN)
+    if max(fill) > window:
+        return plain()
+    total = k * window
     free, _ = torch.cuda.mem_get_info(device)
     if free < total + _ARENA_SLACK_BYTES:
         _log.warning("state arena of %.1f GiB does not fit in %.1f GiB free device memory; "
                      "allocating the masters and moments separately", total / 2**30, free / 2**30)
         return plain()
-    arena = torch.zeros(total, dtype=torch.uint8, device=device)
-    return [arena[o:o + 4 * int(n)].view(torch.float32) for o, n in zip(offsets, numels)]
+    arena = torch.empty(total, dtype=torch.uint8, device=device)
+    out = []
+    for row, offs in zip(sizes, offsets):
+        bufs = []
+        for j, (n, o) in enumerate(zip(row, offs)):
+            start = j * window + o
+            bufs.append(arena[start:start + 4 * int(n)].view(torch.float32).zero_())
+        out.append(bufs)
+    return out
 
 
 # --------------------------------------------------------------------------
@@ -305,7 +336,7 @@ class FlatParamGroup:
         world_size: int,
         zero_stage: int,
         device: torch.device,
-        state_spacing: int = 0,
+        state: Optional[Sequence[torch.Tensor]] = None,
     ):
         device = torch.device(device)
         if len(params) == 0:
@@ -327,19 +358,24 @@ class FlatParamGroup:
         self.shard_size = lay.shard_size
         self.shard_start, self.shard_end = lay.shard_start, lay.shard_end
 
-        # the masters and the AdamW moments of the owned range are streamed
-        # together by the fused AdamW kernel: allocate them as one spaced trio
-        # (see spaced_buffers); the optimizer takes the moments
-        n_own = lay.shard_end - lay.shard_start
+        # the masters and the AdamW moments of the owned range, which the
+        # fused AdamW kernel streams together: given (placed by
+        # state_buffers) or allocated here; the optimizer takes the moments
+        sizes = state_sizes(lay, zero_stage)
+        if state is None:
+            state = state_buffers([sizes], device, 0)[0]
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        if tuple(int(t.numel()) for t in state) != sizes or any(
+                t.dtype != torch.float32 or t.device.type != "cuda" or t.device.index != index
+                for t in state):
+            raise ValueError(f"state buffers must be fp32 on cuda:{index} with {sizes} elements")
         self._master_shard: Optional[torch.Tensor] = None
-        if zero_stage >= 3 and n_own != self.numel_padded:
+        if sizes[0] != self.numel_padded:
             # the masters shrink to the owned range in partition_params
-            self._master_shard, exp_avg, exp_avg_sq = spaced_buffers(
-                [n_own, n_own, n_own], device, state_spacing)
+            self._master_shard, exp_avg, exp_avg_sq = state
             self.data = torch.zeros(self.numel_padded, dtype=torch.float32, device=device)
         else:
-            self.data, exp_avg, exp_avg_sq = spaced_buffers(
-                [self.numel_padded, n_own, n_own], device, state_spacing)
+            self.data, exp_avg, exp_avg_sq = state
         self._moments: Optional[Tuple[torch.Tensor, torch.Tensor]] = (exp_avg, exp_avg_sq)
         self.grad: Optional[torch.Tensor] = (
             None if zero_stage >= 3 else torch.zeros(self.numel_padded, dtype=torch.float32, device=device)
@@ -779,18 +815,25 @@ def build_flat_groups(
     state_spacing: int = 0,
 ) -> Tuple[List[FlatParamGroup], List[dict]]:
     """torch-style group dicts -> FlatParamGroups + option dicts
-    (flat.py:263-291)."""
-    flat_groups: List[FlatParamGroup] = []
-    option_groups: List[dict] = []
+    (flat.py:263-291).  The groups' masters and moments are placed together
+    by ``state_buffers`` (one arena of ``state_spacing``-byte windows, or
+    separate allocations when it is 0)."""
+    device = torch.device(device)
+    kept: List[Tuple[List[nn.Parameter], dict]] = []
     for group in param_groups:
         params = [p for p in group["params"] if p.requires_grad]
         if not params:
             continue
-        flat_groups.append(
-            FlatParamGroup(params, rank=rank, world_size=world_size, zero_stage=zero_stage, device=device,
-                           state_spacing=state_spacing)
-        )
-        option_groups.append({k: v for k, v in group.items() if k != "params"})
-    if not flat_groups:
+        kept.append((params, {k: v for k, v in group.items() if k != "params"}))
+    if not kept:
         raise ValueError("No trainable parameters found")
-    return flat_groups, option_groups
+    sizes = [state_sizes(FlatLayout([p.numel() for p in params], rank=rank, world_size=world_size,
+                                    zero_stage=zero_stage), zero_stage)
+             for params, _ in kept]
+    states = state_buffers(sizes, device, state_spacing)
+    flat_groups = [
+        FlatParamGroup(params, rank=rank, world_size=world_size, zero_stage=zero_stage, device=device,
+                       state=state)
+        for (params, _), state in zip(kept, states)
+    ]
+    return flat_groups, [opts for _, opts in kept]

@@ -436,30 +436,56 @@ def test_zero_size_parameter_in_the_list(stage):
     assert [tuple(p.shape) for p in params] == shapes
 
 
-def test_spaced_state_buffers_are_views_of_one_arena():
-    """With a spacing the buffers are zeroed views of one allocation, each
-    starting max(spacing, previous size) bytes (rounded up to 2 MiB) after the
-    previous one; without, separate allocations."""
-    from minispeed_amd.flat import spaced_buffers
+def test_state_arena_windows():
+    """With a window the buffers are zeroed views of one allocation of three
+    windows: array j of every group in window j, the groups back to back at
+    the same offsets (2 MiB aligned); a column larger than a window, or no
+    window, gives separate allocations."""
+    from minispeed_amd.flat import state_buffers
 
     dev = torch.device(DEV)
     mib = 1 << 20
-    n = 3 * mib + 5                 # 12 MiB + 20 bytes: larger than the spacing below
+    win = 8 * mib
+    sizes = [[1000, 700, 700], [mib // 4 + 3, mib // 4 + 3, 5]]
     torch.cuda.synchronize()
     before = torch.cuda.memory_allocated(dev)
-    bufs = spaced_buffers([1000, n, 1000], dev, 8 * mib)
+    bufs = state_buffers(sizes, dev, win)
     torch.cuda.synchronize()
-    assert [b.numel() for b in bufs] == [1000, n, 1000]
-    assert all(b.dtype == torch.float32 and b.is_contiguous() and int(b.count_nonzero()) == 0 for b in bufs)
-    base = bufs[0].untyped_storage().data_ptr()
-    assert all(b.untyped_storage().data_ptr() == base for b in bufs)
-    assert bufs[1].data_ptr() - bufs[0].data_ptr() == 8 * mib
-    assert bufs[2].data_ptr() - bufs[1].data_ptr() == 14 * mib      # 4n rounded up to 2 MiB
-    assert torch.cuda.memory_allocated(dev) - before >= 22 * mib + 4000
-    bufs[1].fill_(1.0)
-    assert int(bufs[0].count_nonzero()) == 0 and int(bufs[2].count_nonzero()) == 0
-    plain = spaced_buffers([1000, 1000, 1000], dev, 0)
+    assert [[b.numel() for b in row] for row in bufs] == sizes
+    flat_bufs = [b for row in bufs for b in row]
+    assert all(b.dtype == torch.float32 and b.is_contiguous() and int(b.count_nonzero()) == 0
+               for b in flat_bufs)
+    base = bufs[0][0].data_ptr()
+    assert all(b.untyped_storage().data_ptr() == base for b in flat_bufs)
+    for j in range(3):
+        assert bufs[0][j].data_ptr() - base == j * win
+        assert bufs[1][j].data_ptr() - base == j * win + 2 * mib     # after group 0's 2 MiB slot
+    assert torch.cuda.memory_allocated(dev) - before == 3 * win
+    bufs[1][1].fill_(1.0)
+    assert all(int(b.count_nonzero()) == 0 for b in flat_bufs if b is not bufs[1][1])
+    big = state_buffers([[3 * mib, 10, 10]], dev, win)[0]              # 12 MiB > 8 MiB window
+    assert len({b.untyped_storage().data_ptr() for b in big}) == 3
+    plain = state_buffers([[1000, 1000, 1000]], dev, 0)[0]
     assert len({b.untyped_storage().data_ptr() for b in plain}) == 3
+
+
+def test_two_groups_share_one_arena():
+    module = nn.Sequential(nn.Linear(64, 32), nn.Linear(32, 8)).to(DEV)
+    decay = [p for n, p in module.named_parameters() if n.endswith("weight")]
+    no_decay = [p for n, p in module.named_parameters() if n.endswith("bias")]
+    cfg = config(dtype="bf16", stage=1, gas=1)
+    cfg["hip_boundary"] = {"state_spacing_gib": 0.01}
+    engine = ms.initialize(model=module, model_parameters=[{"params": decay},
+                                                           {"params": no_decay, "weight_decay": 0.0}],
+                           config=cfg)
+    g0, g1 = engine.flat_groups
+    st0, st1 = engine.optimizer.state
+    base = g0.data.untyped_storage().data_ptr()
+    for t in (g0.data, g1.data, st0["exp_avg"], st1["exp_avg"], st0["exp_avg_sq"], st1["exp_avg_sq"]):
+        assert t.untyped_storage().data_ptr() == base
+    win = st0["exp_avg"].data_ptr() - g0.data.data_ptr()
+    assert win > 0 and st0["exp_avg_sq"].data_ptr() - st0["exp_avg"].data_ptr() == win
+    assert st1["exp_avg"].data_ptr() - g1.data.data_ptr() == win
 
 
 @pytest.mark.parametrize("stage", [1, 3])
