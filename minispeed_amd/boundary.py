@@ -29,7 +29,7 @@ import numpy as np
 import torch
 
 from . import _native
-from .flat import FlatParamGroup, check_table
+from .flat import FlatParamGroup
 
 
 def _f32(x: float) -> float:
