@@ -58,7 +58,7 @@ def adamw_params(
     hp.eps = _f32(float(eps))
     hp.grad_scale = _f32(grad_scale)
     hp.decay = 1 if wd != 0.0 else 0
-    hp.unscale = 1 if unscale else 0
+    hp.unscale = _native.SCALE_DIVIDE if unscale else _native.SCALE_NONE
     return hp
 
 
@@ -230,7 +230,8 @@ def run_boundary(
         psum, pflag = ws.partial_ptrs(gi)
         tok = timer.start("k1")
         rc = lib.ms_grad_stats(
-            t1[0], t1[1], gdtype, 0, g.numel_padded, lo, hi, 1 if unscale else 0, scale32,
+            t1[0], t1[1], gdtype, 0, g.numel_padded, lo, hi,
+            _native.SCALE_DIVIDE if unscale else _native.SCALE_NONE, scale32,
             flat_out.data_ptr() if flat_out is not None else None,
             psum, pflag, ws.nblk, stream,
         )

@@ -200,7 +200,10 @@ class SegmentTable:
     that overwrites a replaced entry is queued on the stream of the
     boundary that uploads it, after every kernel of the earlier boundaries
     that read the entry: the boundaries of one engine run on one stream, or
-    the new stream first waits for the old one (``Workspace.enter``).
+    the new stream first waits for the old one (``Workspace.enter``).  Every
+    use records the current stream on the device table, so that when an
+    entry is dropped torch's caching allocator does not hand its memory to
+    another stream before the kernels that read it have run.
     """
 
     SLOTS = 4
@@ -214,9 +217,11 @@ class SegmentTable:
         n = int(table.shape[0])
         if n == 0:
             return 0, 0
+        stream = torch.cuda.current_stream(self.device)
         for k, (host, dev) in enumerate(self._entries):
             if host.shape == table.shape and np.array_equal(host, table):
                 self._entries.append(self._entries.pop(k))
+                dev.record_stream(stream)
                 return dev.data_ptr(), n
         staging = torch.empty((n, 4), dtype=torch.int64, pin_memory=True)
         staging.numpy()[:] = table
@@ -227,6 +232,7 @@ class SegmentTable:
         else:
             dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
         dev.copy_(staging, non_blocking=True)
+        dev.record_stream(stream)
         self._entries.append((table.copy(), dev))
         return dev.data_ptr(), n
 
