@@ -294,35 +294,42 @@ def state_buffers(sizes: Sequence[Sequence[int]], device: torch.device,
     def plain() -> List[List[torch.Tensor]]:
         return [[torch.zeros(int(n), dtype=torch.float32, device=device) for n in row] for row in sizes]
 
-    if window <= 0 or not sizes:
+    layout = arena_layout(sizes, window)
+    if layout is None:
         return plain()
-    k = len(sizes[0])
-    if any(len(row) != k for row in sizes):
-        raise ValueError("every group needs the same number of state arrays")
-    window = _round_up(int(window), _ARENA_ALIGN)
-    fill = [0] * k
-    offsets = []
-    for row in sizes:
-        offsets.append(list(fill))
-        for j, n in enumerate(row):
-            fill[j] += _round_up(4 * int(n), _ARENA_ALIGN)
-    if max(fill) > window:
-        return plain()
-    total = k * window
+    starts, total = layout
     free, _ = torch.cuda.mem_get_info(device)
     if free < total + _ARENA_SLACK_BYTES:
         _log.warning("state arena of %.1f GiB does not fit in %.1f GiB free device memory; "
                      "allocating the masters and moments separately", total / 2**30, free / 2**30)
         return plain()
     arena = torch.empty(total, dtype=torch.uint8, device=device)
-    out = []
-    for row, offs in zip(sizes, offsets):
-        bufs = []
-        for j, (n, o) in enumerate(zip(row, offs)):
-            start = j * window + o
-            bufs.append(arena[start:start + 4 * int(n)].view(torch.float32).zero_())
-        out.append(bufs)
-    return out
+    return [[arena[a:a + 4 * int(n)].view(torch.float32).zero_() for n, a in zip(row, row_starts)]
+            for row, row_starts in zip(sizes, starts)]
+
+
+def arena_layout(sizes: Sequence[Sequence[int]],
+                 window: int) -> Optional[Tuple[List[List[int]], int]]:
+    """Byte offsets of ``state_buffers``' arena: ``(starts, total)`` with
+    ``starts[g][j]`` the start of array j of group g (fp32 elements
+    ``sizes[g][j]``) and ``total`` the arena size, or None for separate
+    allocations (no window, nothing to place, or a column that does not fit
+    in one window).  Windows and slots are rounded up to 2 MiB."""
+    if window <= 0 or not sizes:
+        return None
+    k = len(sizes[0])
+    if any(len(row) != k for row in sizes):
+        raise ValueError("every group needs the same number of state arrays")
+    window = _round_up(int(window), _ARENA_ALIGN)
+    fill = [0] * k
+    starts = []
+    for row in sizes:
+        starts.append([j * window + fill[j] for j in range(k)])
+        for j, n in enumerate(row):
+            fill[j] += _round_up(4 * int(n), _ARENA_ALIGN)
+    if max(fill) > window:
+        return None
+    return starts, k * window
 
 
 # --------------------------------------------------------------------------

@@ -139,3 +139,28 @@ def test_gpt_workload_shapes_match_reference_counts():
         d = s[2][0]
         for block in itertools.islice(zip(*[iter(s[2:-2])] * 12), 2):
             assert block[2] == (3 * d, d) and block[8] == (4 * d, d) and block[10] == (d, 4 * d)
+
+
+def test_state_arena_layout():
+    """Array j of every group in window j, groups back to back at equal
+    offsets, 2 MiB slots; None when a column overflows its window."""
+    from minispeed_amd.flat import arena_layout
+
+    mib = 1 << 20
+    starts, total = arena_layout([[1000, 700, 700], [mib // 4 + 3, mib // 4 + 3, 5]], 8 * mib)
+    assert total == 24 * mib
+    assert starts == [[0, 8 * mib, 16 * mib], [2 * mib, 10 * mib, 18 * mib]]
+    # an 11 MiB window is rounded up to 12 MiB
+    assert arena_layout([[1, 1, 1]], 11 * mib) == ([[0, 12 * mib, 24 * mib]], 36 * mib)
+    # one column just fits, then overflows
+    assert arena_layout([[2 * mib, 1, 1], [2 * mib, 1, 1]], 4 * mib * 4) is not None
+    assert arena_layout([[3 * mib, 1, 1]], 8 * mib) is None          # 12 MiB > 8 MiB
+    assert arena_layout([[1, 1, 1]], 0) is None
+    assert arena_layout([], 8 * mib) is None
+    import pytest
+    with pytest.raises(ValueError):
+        arena_layout([[1, 1, 1], [1, 1]], 8 * mib)
+    # the 1.3B GPT state at 32 GiB: three windows, 96 GiB
+    n = 1_315_723_264
+    starts, total = arena_layout([[n, n, n]], 32 << 30)
+    assert starts == [[0, 32 << 30, 64 << 30]] and total == 96 << 30
