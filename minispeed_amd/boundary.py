@@ -94,8 +94,9 @@ class Workspace:
         torch.cuda.current_stream(self.device).synchronize()
         return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
 
-    def enter(self) -> None:
-        """Called at the start of a boundary.  Kernels of the previous
+    def enter(self) -> torch.cuda.Stream:
+        """Called at the start of a boundary; returns the current stream,
+        which the boundary's kernels run on.  Kernels of the previous
         boundary (K3 reading the scalars and segment tables this boundary
         overwrites) may still run on its stream; if the current stream is
         another one, it first waits for everything queued there."""
@@ -103,6 +104,7 @@ class Workspace:
         if self._stream is not None and self._stream != cur:
             cur.wait_stream(self._stream)
         self._stream = cur
+        return cur
 
     def start_readback(self) -> None:
         """Mark the end of K2 (just launched on the current stream with
@@ -207,8 +209,8 @@ def run_boundary(
     """
     lib = _native.load()
     device = ws.device
-    ws.enter()
-    stream = _native.stream_handle(device)
+    cur = ws.enter()
+    stream = cur.cuda_stream
     scale = float(scaler.loss_scale_factor)
     unscale = scale != 1.0
     scale32 = _f32(scale)
@@ -226,7 +228,7 @@ def run_boundary(
             flat_out = g.grad
             g._grad_dirty = True
         lo, hi = g.own_range
-        t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None))
+        t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None), cur)
         psum, pflag = ws.partial_ptrs(gi)
         tok = timer.start("k1")
         rc = lib.ms_grad_stats(
@@ -265,7 +267,7 @@ def run_boundary(
                 f"grad/shard shape mismatch: owned range {hi - lo} vs master {master.numel()}, "
                 f"moments {gl.exp_avg.numel()}/{gl.exp_avg_sq.numel()}"
             )
-        t3 = g.table("k3").upload(g.boundary_table(lo, hi, gl.grads, mptrs))
+        t3 = g.table("k3").upload(g.boundary_table(lo, hi, gl.grads, mptrs), cur)
         hp = adamw_params(gl.lr, gl.betas, gl.eps, gl.weight_decay, gl.step,
                           grad_scale=scale, unscale=unscale and flat_out is None)
         fg_ptr = flat_out.data_ptr() + lo * 4 if flat_out is not None else None

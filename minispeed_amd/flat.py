@@ -210,30 +210,39 @@ class SegmentTable:
 
     def __init__(self, device: torch.device):
         self.device = device
-        self._entries: List[Tuple[np.ndarray, torch.Tensor]] = []   # most recent last
+        # (host table, device table, streams recorded on it); most recent last
+        self._entries: List[Tuple[np.ndarray, torch.Tensor, set]] = []
 
-    def upload(self, table: np.ndarray) -> Tuple[int, int]:
-        """Return (device pointer, row count)."""
+    def upload(self, table: np.ndarray, stream: Optional[torch.cuda.Stream] = None) -> Tuple[int, int]:
+        """Return (device pointer, row count) of ``table`` for kernels
+        queued on ``stream`` (default: the current stream)."""
         n = int(table.shape[0])
         if n == 0:
             return 0, 0
-        stream = torch.cuda.current_stream(self.device)
-        for k, (host, dev) in enumerate(self._entries):
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        for k, entry in enumerate(self._entries):
+            host, dev, seen = entry
             if host.shape == table.shape and np.array_equal(host, table):
                 self._entries.append(self._entries.pop(k))
-                dev.record_stream(stream)
+                if stream.cuda_stream not in seen:
+                    dev.record_stream(stream)
+                    seen.add(stream.cuda_stream)
                 return dev.data_ptr(), n
         staging = torch.empty((n, 4), dtype=torch.int64, pin_memory=True)
         staging.numpy()[:] = table
+        seen = set()
         if len(self._entries) >= self.SLOTS:
-            _, dev = self._entries.pop(0)
+            _, dev, seen = self._entries.pop(0)
             if dev.shape[0] != n:
-                dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
+                dev, seen = torch.empty((n, 4), dtype=torch.int64, device=self.device), set()
         else:
             dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
         dev.copy_(staging, non_blocking=True)
-        dev.record_stream(stream)
-        self._entries.append((table.copy(), dev))
+        if stream.cuda_stream not in seen:
+            dev.record_stream(stream)
+            seen.add(stream.cuda_stream)
+        self._entries.append((table.copy(), dev, seen))
         return dev.data_ptr(), n
 
 
