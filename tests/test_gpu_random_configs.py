@@ -1,0 +1,176 @@
+"""Seeded random configurations of the whole boundary against the oracle.
+
+Each case draws a parameter list (ragged sizes, one or two groups with their
+own lr / weight decay / betas / eps), a dtype, a ZeRO stage, a clip value, a
+loss scale and a WarmupDecayLR schedule, then runs boundaries with fresh
+random gradients, some parameters without a gradient and, on one step, an
+inf or NaN in one gradient.  Before every boundary the oracle (the torch-CPU
+restatement of engine.py:268-322) is loaded with the GPU's state; after it:
+
+* the GPU and the oracle agree on whether the step was applied, on the
+  loss-scaler state and on the gradient norm (1e-5 relative);
+* the GPU's masters, exp_avg and exp_avg_sq equal, bit for bit, the kernel
+  recipe (oracle.recipe: the same op order with a correctly rounded sqrt)
+  applied with the GPU's own clip coefficient;
+* when that coefficient equals the oracle's, the moments equal the oracle's
+  bit for bit and the masters are within 2 fp32 ulp of max(|p_before|,
+  |p_after|) (torch's CPU sqrt is not correctly rounded); when the two
+  norms round to different coefficients (fp64 against a CPU fp32 cascade
+  sum) a cancellation in exp_avg can magnify that one-ulp difference, and
+  the norm bound is the check;
+* the model copy is bit for bit the cast of the masters;
+* a skipped step leaves the masters and moments untouched, bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import minispeed_amd as ms
+from oracle import boundary as ob
+from oracle import recipe
+from tests.helpers import DEV, master_step_within_ulps
+
+pytestmark = pytest.mark.gpu
+
+TORCH_DTYPE = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _draw(seed):
+    rng = np.random.default_rng(seed)
+    dtype = ["fp32", "fp16", "bf16"][seed % 3]
+    stage = int(rng.integers(0, 4))
+    clip = [None, 0.05, 1.0, 1e3][int(rng.integers(0, 4))]
+    ngroups = int(rng.integers(1, 3))
+    nparams = int(rng.integers(2, 9))
+    sizes = [int(x) for x in rng.integers(1, 5000, size=nparams)]
+    sizes[int(rng.integers(0, nparams))] = int(rng.integers(1, 9))    # a tiny one
+    split = int(rng.integers(1, nparams)) if ngroups == 2 else nparams
+    groups = [list(range(split))] + ([list(range(split, nparams))] if ngroups == 2 else [])
+    opts = []
+    for _ in groups:
+        opts.append({"lr": float(rng.choice([1e-4, 1e-3, 1e-2])),
+                     "weight_decay": float(rng.choice([0.0, 0.01, 0.1])),
+                     "betas": [(0.9, 0.999), (0.8, 0.95)][int(rng.integers(0, 2))],
+                     "eps": float(rng.choice([1e-8, 1e-6]))})
+    power = int(rng.integers(6, 17))
+    warmup = int(rng.integers(0, 4))
+    return dict(dtype=dtype, stage=stage, clip=clip, sizes=sizes, groups=groups, opts=opts,
+                power=power, warmup=warmup, inject=int(rng.integers(0, 4)), rng=rng)
+
+
+def _config(c, max_lr):
+    cfg = {"train_micro_batch_size_per_gpu": 1, "gradient_accumulation_steps": 1,
+           "gradient_clipping": c["clip"] or 0.0, "dtype": c["dtype"],
+           "optimizer": {"type": "AdamW", "params": {"lr": max_lr, "betas": [0.9, 0.999],
+                                                      "eps": 1e-8, "weight_decay": 0.0}},
+           "scheduler": {"type": "WarmupDecayLR",
+                         "params": {"warmup_min_lr": 0.0, "warmup_max_lr": max_lr,
+                                    "warmup_num_steps": c["warmup"], "total_num_steps": 20}},
+           "zero_optimization": {"stage": c["stage"]}, "steps_per_print": 1000}
+    if c["dtype"] == "fp16":
+        cfg["fp16"] = {"enabled": True, "loss_scale": 0, "initial_scale_power": c["power"],
+                       "loss_scale_window": 2}
+    return cfg
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configuration_against_the_oracle(seed):
+    c = _draw(seed)
+    rng = c["rng"]
+    tdt = TORCH_DTYPE[c["dtype"]]
+    gen = torch.Generator().manual_seed(seed)
+    init = [torch.randn(n, generator=gen) * 0.02 for n in c["sizes"]]
+    params = [nn.Parameter(t.clone().to(DEV)) for t in init]
+    ref_params = [nn.Parameter(t.clone()) for t in init]
+    max_lr = c["opts"][0]["lr"]
+    engine = ms.initialize(
+        model=nn.ParameterList(params),
+        model_parameters=[dict(o, params=[params[i] for i in idx]) for idx, o in zip(c["groups"], c["opts"])],
+        config=_config(c, max_lr))
+    ref = ob.Engine([[ref_params[i] for i in idx] for idx in c["groups"]], c["opts"], dtype=c["dtype"],
+                    zero_stage=c["stage"], clip=c["clip"], initial_scale_power=c["power"],
+                    loss_scale_window=2, scheduler="WarmupDecayLR",
+                    scheduler_params={"warmup_min_lr": 0.0, "warmup_max_lr": max_lr,
+                                      "warmup_num_steps": c["warmup"], "total_num_steps": 20})
+    opt = engine.optimizer
+    scale_mult = 1.0
+    for step in range(4):
+        if c["stage"] >= 3:
+            opt.gather_parameters()
+        before = [g.data.detach().cpu().clone() for g in engine.flat_groups]
+        m_before = [st["exp_avg"].cpu() for st in opt.state]
+        v_before = [st["exp_avg_sq"].cpu() for st in opt.state]
+        ref.load_state(before, m_before, v_before, [st["step"] for st in opt.state],
+                       (engine.loss_scaler.scale, engine.loss_scaler.good_steps,
+                        engine.loss_scaler.skipped_steps),
+                       engine.lr_scheduler.last_epoch, [pg["lr"] for pg in opt.param_groups])
+        if c["stage"] >= 3:
+            ref.gather_parameters()          # from the loaded masters
+        if c["dtype"] == "fp16":
+            scale_mult = engine.loss_scaler.scale
+        scale_before = engine.loss_scaler.loss_scale_factor
+        lrs_before = [pg["lr"] for pg in opt.param_groups]
+        grads = []
+        for i, (p, rp) in enumerate(zip(params, ref_params)):
+            if rng.random() < 0.15:
+                p.grad = rp.grad = None
+                grads.append(None)
+                continue
+            gr = (torch.randn(c["sizes"][i], generator=gen) * 1e-2 * scale_mult).to(tdt)
+            if step == c["inject"] and i == 0:
+                gr[int(rng.integers(0, gr.numel()))] = float(rng.choice([np.inf, -np.inf, np.nan]))
+            p.grad = gr.to(DEV)
+            rp.grad = gr.clone()
+            grads.append(gr)
+        engine.micro_steps += 1
+        ref.micro_steps += 1
+        applied, ref_applied = engine.step(), ref.step()
+        assert applied == ref_applied, (seed, step)
+        s = engine.loss_scaler
+        assert (s.scale, s.good_steps, s.skipped_steps) == (ref.scaler.scale, ref.scaler.good_steps,
+                                                            ref.scaler.skipped_steps)
+        if not applied:
+            for g, b in zip(engine.flat_groups, before):
+                assert torch.equal(g.data.cpu().view(torch.int32), b.view(torch.int32))
+            for st, m, v in zip(opt.state, m_before, v_before):
+                assert torch.equal(st["exp_avg"].cpu(), m) and torch.equal(st["exp_avg_sq"].cpu(), v)
+            continue
+        assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * max(ref.grad_norm, 1e-30)
+        res = engine.last_boundary
+        gpu_coef = np.float32(res.coef) if res.clip_applied else None
+        same = True
+        if c["clip"] is not None and ref.grad_norm > c["clip"]:
+            _, _, coef = recipe.clip_coef(np.float32(ref.grad_norm), c["clip"])
+            same = gpu_coef is not None and gpu_coef == np.float32(coef)
+        for gi, (g, idx) in enumerate(zip(engine.flat_groups, c["groups"])):
+            flat = np.zeros(g.numel_padded, dtype=np.float32)
+            for (off, _), n, i in zip(g._offsets, g._numels, idx):
+                if grads[i] is not None:
+                    flat[off:off + n] = grads[i].float().numpy()
+            o = c["opts"][gi]
+            wp, wm, wv = recipe.adamw_step(before[gi].numpy(), m_before[gi].numpy(), v_before[gi].numpy(),
+                                           flat, lr=lrs_before[gi], betas=o["betas"], eps=o["eps"],
+                                           wd=o["weight_decay"], step=opt.state[gi]["step"],
+                                           grad_scale=scale_before, unscale=scale_before != 1.0,
+                                           clip_coef=gpu_coef)
+            st = opt.state[gi]
+            for got, want in ((g.data, wp), (st["exp_avg"], wm), (st["exp_avg_sq"], wv)):
+                np.testing.assert_array_equal(got.cpu().numpy().view(np.int32), want.view(np.int32))
+            if same:
+                ok, worst = master_step_within_ulps(before[gi].numpy(), g.data.cpu().numpy(),
+                                                    ref.groups[gi].data.numpy(), 2.0)
+                assert ok, (seed, step, gi, worst)
+                assert torch.equal(st["exp_avg"].cpu(), ref.state[gi]["exp_avg"])
+                assert torch.equal(st["exp_avg_sq"].cpu(), ref.state[gi]["exp_avg_sq"])
+        if c["stage"] >= 3:
+            opt.gather_parameters()
+        for g in engine.flat_groups:
+            master = g.data.cpu()
+            for (off, p), n in zip(g._offsets, g._numels):
+                want = master[off:off + n].to(tdt)
+                assert torch.equal(p.detach().cpu().reshape(-1).view(torch.uint8),
+                                   want.view(torch.uint8)), (seed, step, off)
