@@ -77,7 +77,7 @@ def _config(c, max_lr):
     return cfg
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(96))
 def test_random_configuration_against_the_oracle(seed):
     c = _draw(seed)
     rng = c["rng"]
