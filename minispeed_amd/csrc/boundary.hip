@@ -2,8 +2,9 @@
 // boundary step and the C ABI declared in include/minispeed_boundary.h.
 //
 //   K1 k_grad_stats   ragged grad scan: inf/nan flag on the raw values,
-//                     unscale, optional fp32 flat write, per-block fp64
-//                     sum of squares            (flat.py:196-247)
+//                     unscale (or a clip multiply), optional fp32 flat
+//                     write, per-block fp64 sum of squares
+//                                               (flat.py:196-257)
 //   K2 k_norm_clip    deterministic second-level reduction, clip
 //                     coefficient, skip flag, loss-scale update
 //                                               (stage_1_and_2.py:105-128,
@@ -699,7 +700,7 @@ int launch_status() {
   return e == hipSuccess ? MS_OK : static_cast<int>(e);
 }
 
-// How a kernel divides by the loss scale (see unscale1).  `unscale` is
+// How a kernel scales each widened gradient (see unscale1).  `unscale` is
 // MS_SCALE_NONE, MS_SCALE_DIVIDE or MS_SCALE_MULTIPLY (checked by the caller).
 int unscale_mode(int32_t unscale, float scale, float* inv) {
   *inv = 1.0f;
