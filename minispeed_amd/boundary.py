@@ -228,7 +228,8 @@ def run_boundary(
             flat_out = g.grad
             g._grad_dirty = True
         lo, hi = g.own_range
-        t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None), cur)
+        gbytes = 4 if gdtype == _native.DTYPE_F32 else 2
+        t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None, gbytes), cur)
         psum, pflag = ws.partial_ptrs(gi)
         tok = timer.start("k1")
         rc = lib.ms_grad_stats(
@@ -239,7 +240,7 @@ def run_boundary(
         )
         timer.stop(tok)
         _native.check(rc, "ms_grad_stats")
-        dtypes.append((gdtype, dtype))
+        dtypes.append((gdtype, dtype, gbytes))
         flats.append(flat_out)
 
     tok = timer.start("k2")
@@ -256,7 +257,7 @@ def run_boundary(
     ws.start_readback()
 
     models = model_targets()
-    for gl, (gdtype, dtype), flat_out, mptrs in zip(launches, dtypes, flats, models):
+    for gl, (gdtype, dtype, gbytes), flat_out, mptrs in zip(launches, dtypes, flats, models):
         g = gl.group
         lo, hi = g.own_range
         if hi <= lo:
@@ -267,7 +268,7 @@ def run_boundary(
                 f"grad/shard shape mismatch: owned range {hi - lo} vs master {master.numel()}, "
                 f"moments {gl.exp_avg.numel()}/{gl.exp_avg_sq.numel()}"
             )
-        t3 = g.table("k3").upload(g.boundary_table(lo, hi, gl.grads, mptrs), cur)
+        t3 = g.table("k3").upload(g.boundary_table(lo, hi, gl.grads, mptrs, gbytes), cur)
         hp = adamw_params(gl.lr, gl.betas, gl.eps, gl.weight_decay, gl.step,
                           grad_scale=scale, unscale=unscale and flat_out is None)
         fg_ptr = flat_out.data_ptr() + lo * 4 if flat_out is not None else None

@@ -671,10 +671,12 @@ class FlatParamGroup:
         return ptrs
 
     def boundary_table(self, lo: int, hi: int, gptrs: Optional[List[int]],
-                       mptrs: Optional[List[int]]) -> np.ndarray:
+                       mptrs: Optional[List[int]], grad_elem_bytes: Optional[int] = None) -> np.ndarray:
         """Segment table of ``[lo, hi)`` with the given grad / model
-        addresses (``None``: no such storage).  For the whole padded range
-        with full-size parameters the rows are static and only the two
+        addresses (``None``: no such storage); the gradient storage holds
+        ``grad_elem_bytes``-byte elements (default: the parameters' size;
+        4 for the fp32 sums of contiguous gradients).  For the whole padded
+        range with full-size parameters the rows are static and only the two
         pointer columns are filled in."""
         n_params = len(self.params)
         full = True
@@ -701,7 +703,7 @@ class FlatParamGroup:
             if mptrs is not None:
                 table[:, 3] = _with_pad_slot(mptrs, n_params)[idx]
             return table
-        esz_g = _ELEM_BYTES[self.model_dtype()]
+        esz_g = grad_elem_bytes or _ELEM_BYTES[self.model_dtype()]
         grads = [None] * n_params
         models = [None] * n_params
         for i, ((off, p), n) in enumerate(zip(self._offsets, self._numels)):

@@ -524,3 +524,20 @@ def test_engine_takes_the_moments_allocated_with_the_masters():
     assert g.take_moment_buffers() is None            # handed to the optimizer
     st = engine.optimizer.state[0]
     assert st["exp_avg"].numel() == st["exp_avg_sq"].numel() == g.numel_shard()
+
+
+def test_owned_range_table_uses_the_gradient_element_size():
+    """A table over one rank's range starts rows mid-parameter; the gradient
+    address of such a row advances by the gradient's element size (4 for the
+    fp32 sums of contiguous gradients, 2 for fp16 parameters' own grads)."""
+    params = [nn.Parameter(torch.zeros(n, dtype=torch.float16, device=DEV)) for n in (10, 7, 13)]
+    g = FlatParamGroup(params, rank=1, world_size=2, zero_stage=1, device=torch.device(DEV))
+    lo, hi = g.own_range                                   # [15, 30): starts inside param 1
+    assert (lo, hi) == (15, 30)
+    gptrs = [1 << 20, 2 << 20, 3 << 20]
+    for esize in (4, 2, None):
+        table = g.boundary_table(lo, hi, gptrs, None, esize)
+        step = esize or 2
+        rows = {int(b): (int(n), int(gp)) for b, n, gp, _ in table}
+        assert rows[15] == (2, (2 << 20) + (15 - 10) * step)     # param 1, elements 5..6
+        assert rows[17] == (13, 3 << 20)                          # param 2 from its start
