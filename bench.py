@@ -75,6 +75,8 @@ def parse(argv=None):
                     help="time the steps without the per-kernel HIP events (no roofline)")
     ap.add_argument("--cpu-sample-params", type=int, default=0,
                     help="CPU baseline sample (0: the whole workload, ~1 minute at 1.3B)")
+    ap.add_argument("--hbm-ceilings", action="store_true",
+                    help="measure streaming-bandwidth reference points instead of the boundary step")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (a counter yardstick for rocprofv3 --pmc)")
     return ap.parse_args(argv)
@@ -329,6 +331,89 @@ def traffic_for(kernel: str, workload: str, grad_dtype: str, mode: str):
     return None if entry is None else entry.get("bytes_per_launch")
 
 
+def bench_hbm_ceilings(args) -> dict:
+    """Streaming-bandwidth reference points on 4 GiB fp32 buffers (1 GiB for
+    the half-precision streams): what one read-only stream, one write-only
+    stream, a 1:1 copy and a 2:1 add reach on this GPU, next to K3 itself
+    over contiguous arrays with the masters and moments in a 32 GiB-window
+    arena and in separate allocations.  Median of 10 launches after 3, HIP
+    events on the current stream; bytes are the algorithmic ones."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from minispeed_amd import _native
+    from minispeed_amd.boundary import adamw_params
+    from minispeed_amd.flat import STATE_SPACING_BYTES, FlatLayout, state_buffers
+
+    lib = _native.load()
+    dev = torch.device("cuda", 0)
+    stream = _native.stream_handle(dev)
+    n = 1 << 30
+
+    def median_ms(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(10):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        return float(np.median([a.elapsed_time(b) for a, b in evs]))
+
+    out = {}
+
+    def record(name, nbytes, ms):
+        out[name] = {"ms": round(ms, 4), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        log(f"[bench] {name}: {ms:.3f} ms, {out[name]['gbps']:.0f} GB/s")
+
+    x = torch.ones(n, device=dev)
+    nb = _native.stats_blocks()
+    psum = torch.empty(nb, dtype=torch.float64, device=dev)
+    pflag = torch.empty(nb, dtype=torch.int32, device=dev)
+    table = torch.from_numpy(np.array([[0, n, x.data_ptr(), 0]], dtype=np.int64)).to(dev)
+
+    def read_only():
+        _native.check(lib.ms_grad_stats(table.data_ptr(), 1, _native.DTYPE_F32, 0, n, 0, n,
+                                        _native.SCALE_NONE, 1.0, None, psum.data_ptr(),
+                                        pflag.data_ptr(), nb, stream), "ms_grad_stats")
+    record("read_only_k1_fp32", 4 * n, median_ms(read_only))
+    record("write_only_fill", 4 * n, median_ms(lambda: x.fill_(1.0)))
+    y = torch.empty_like(x)
+    record("copy_1_to_1", 8 * n, median_ms(lambda: y.copy_(x)))
+    z = torch.empty_like(x)
+    record("add_2_to_1", 12 * n, median_ms(lambda: torch.add(x, y, out=z)))
+    del x, y, z, table
+    torch.cuda.empty_cache()
+
+    g = torch.full((n,), 0.5, dtype=torch.float16, device=dev)
+    model = torch.empty(n, dtype=torch.float16, device=dev)
+    lay = FlatLayout([n], rank=0, world_size=1, zero_stage=1)
+    tab = torch.from_numpy(lay.segments(0, n, [(g.data_ptr(), (0, n), 2)],
+                                        [(model.data_ptr(), (0, n), 2)])).to(dev)
+    hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 10)
+    clean = torch.zeros(_native.SCALARS_BYTES, dtype=torch.uint8, device=dev)
+    for name, window in (("k3_arena_32gib", STATE_SPACING_BYTES), ("k3_separate", 0)):
+        p, m, v = state_buffers([[n, n, n]], dev, window)[0]
+        p.fill_(0.01)
+
+        def k3():
+            _native.check(lib.ms_fused_adamw(p.data_ptr(), m.data_ptr(), v.data_ptr(), None,
+                                             tab.data_ptr(), tab.shape[0], _native.DTYPE_F16,
+                                             _native.DTYPE_F16, 0, n, ctypes.byref(hp),
+                                             clean.data_ptr(), stream), "ms_fused_adamw")
+        record(name, 28 * n, median_ms(k3))
+        del p, m, v
+        torch.cuda.empty_cache()
+    return {"hbm_ceilings": out, "elements": n, "peak_gbps": 8000.0,
+            "note": "fp32 buffers of 4 GiB; K3 moves 28 B per element (fp16 grads and model copy)"}
+
+
 def main(argv=None) -> int:
     args = parse(argv)
     if args.gpus != 1:
@@ -346,6 +431,10 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}))
         return 1
+    if args.hbm_ceilings:
+        torch.cuda.set_device(0)
+        print(json.dumps(bench_hbm_ceilings(args)), flush=True)
+        return 0
     if args.workload == "llama3-8b-shard":
         torch.cuda.set_device(0)
         print(json.dumps(bench_llama_shard(args)), flush=True)
