@@ -8,16 +8,23 @@
          "lr_scheduler", "loss_scaler", "global_steps", "micro_steps",
          "grad_norm", "rank", "world_size"}
 
-The same file names and keys as checkpoint.py:21-125, so a run can resume
-from a checkpoint minispeed wrote and minispeed can resume from one written
-here.  Tensors are stored on the CPU; files are read with
-``torch.load(..., weights_only=True)``.
+File names, keys and the two load errors are minispeed's
+(checkpoint.py:21-125), so either implementation resumes from the other's
+files.  Everything is written as CPU tensors (the flat buffers live in HBM
+here) and read with ``torch.load(..., weights_only=True)``.
+
+The model state needs full-shaped parameters; at ZeRO-3 the parameters are
+placeholders between steps, so both directions run inside
+:func:`_full_parameters`, which gathers them and afterwards returns them to
+the state they were in.
 """
 
 from __future__ import annotations
 
 import os
-from typing import Optional, Tuple
+from contextlib import contextmanager
+from dataclasses import dataclass
+from typing import Iterator, Optional, Tuple
 
 import torch
 
@@ -26,21 +33,13 @@ from . import comm
 MODEL_STATES = "mp_rank_00_model_states.pt"
 LATEST = "latest"
 
+# keys of the per-rank file that are plain engine counters: (key, attribute, cast)
+_COUNTERS = (("global_steps", "global_steps", int), ("micro_steps", "micro_steps", int),
+             ("grad_norm", "grad_norm", None))
+
 
 def optim_states_name(rank: int) -> str:
     return f"zero_pp_rank{rank}_mp_rank_00_optim_states.pt"
-
-
-def _cpu(obj):
-    if isinstance(obj, torch.Tensor):
-        return obj.detach().cpu().clone()
-    if isinstance(obj, dict):
-        return {k: _cpu(v) for k, v in obj.items()}
-    if isinstance(obj, list):
-        return [_cpu(v) for v in obj]
-    if isinstance(obj, tuple):
-        return tuple(_cpu(v) for v in obj)
-    return obj
 
 
 def read_latest(save_dir: str) -> str:
@@ -48,81 +47,117 @@ def read_latest(save_dir: str) -> str:
         return fh.read().strip()
 
 
-@torch.no_grad()
-def save_checkpoint(engine, save_dir: str, tag: Optional[str] = None) -> str:
-    """Write the model state (rank 0), ``latest`` and this rank's optimizer
-    shard; ZeRO-3 parameters are gathered for the model state and freed
-    again afterwards (checkpoint.py:35-71)."""
-    tag = tag or f"global_step{engine.global_steps}"
-    ckpt_dir = os.path.join(save_dir, tag)
-    os.makedirs(ckpt_dir, exist_ok=True)
-    was_gathered = engine.optimizer.params_gathered
-    engine.optimizer.gather_parameters()
-    if engine.rank == 0:
-        torch.save({"module": _cpu(engine.module.state_dict()), "tag": tag},
-                   os.path.join(ckpt_dir, MODEL_STATES))
-        with open(os.path.join(save_dir, LATEST), "w", encoding="utf-8") as fh:
-            fh.write(tag)
-    state = {
-        "optimizer": _cpu(engine.optimizer.state_dict()),
-        "fp32_groups": [g.data.detach().cpu().clone() for g in engine.flat_groups],
+@dataclass(frozen=True)
+class _Where:
+    root: str
+    tag: str
+
+    @property
+    def folder(self) -> str:
+        return os.path.join(self.root, self.tag)
+
+    @property
+    def model_file(self) -> str:
+        return os.path.join(self.folder, MODEL_STATES)
+
+    def shard_file(self, rank: int) -> str:
+        return os.path.join(self.folder, optim_states_name(rank))
+
+
+def _to_host(obj):
+    """Deep copy with every tensor on the CPU (device buffers can be views
+    of larger allocations; a copy stores only their own elements)."""
+    if isinstance(obj, torch.Tensor):
+        return obj.detach().to("cpu", copy=True)
+    if isinstance(obj, (list, tuple)):
+        return type(obj)(_to_host(v) for v in obj)
+    if isinstance(obj, dict):
+        return {k: _to_host(v) for k, v in obj.items()}
+    return obj
+
+
+@contextmanager
+def _full_parameters(engine, refresh: bool = False) -> Iterator[None]:
+    """Full-shaped parameters inside the block; afterwards the ZeRO-3
+    placeholders come back if that is how the block found them.  With
+    ``refresh`` (after new masters were loaded) a ZeRO-3 engine is freed and
+    re-gathered, so the parameters are recast from the masters."""
+    opt = engine.optimizer
+    gathered_before = opt.params_gathered
+    opt.gather_parameters()
+    yield
+    if refresh and engine.config.zero_stage >= 3:
+        opt.free_parameters()
+        if gathered_before:
+            opt.gather_parameters()
+    elif not gathered_before:
+        opt.free_parameters()
+
+
+def _shard_payload(engine) -> dict:
+    payload = {
+        "optimizer": _to_host(engine.optimizer.state_dict()),
+        "fp32_groups": [_to_host(g.data) for g in engine.flat_groups],
         "lr_scheduler": engine.lr_scheduler.state_dict(),
         "loss_scaler": engine.loss_scaler.state_dict(),
-        "global_steps": engine.global_steps,
-        "micro_steps": engine.micro_steps,
-        "grad_norm": engine.grad_norm,
-        "rank": engine.rank,
-        "world_size": engine.world_size,
     }
-    torch.save(state, os.path.join(ckpt_dir, optim_states_name(engine.rank)))
-    comm.barrier()
-    if not was_gathered:
-        engine.optimizer.free_parameters()
-    return ckpt_dir
+    payload.update({key: getattr(engine, attr) for key, attr, _ in _COUNTERS})
+    payload["rank"], payload["world_size"] = engine.rank, engine.world_size
+    return payload
 
 
-@torch.no_grad()
-def load_checkpoint(engine, load_dir: str, tag: Optional[str] = None) -> Tuple[str, dict]:
-    """Restore model, masters, optimizer shard, scheduler, scaler and
-    counters (checkpoint.py:74-125).  Masters are restored from the saved
-    fp32 buffers and cast into the model parameters on the GPU."""
-    tag = tag or read_latest(load_dir)
-    ckpt_dir = os.path.join(load_dir, tag)
-    was_gathered = engine.optimizer.params_gathered
-    engine.optimizer.gather_parameters()
-
-    model_state = torch.load(os.path.join(ckpt_dir, MODEL_STATES), map_location="cpu",
-                             weights_only=True)
-    engine.module.load_state_dict(model_state["module"])
-
-    optim_path = os.path.join(ckpt_dir, optim_states_name(engine.rank))
-    if not os.path.exists(optim_path):
-        raise FileNotFoundError(f"Missing optimizer shard for rank {engine.rank}: {optim_path}")
-    state = torch.load(optim_path, map_location="cpu", weights_only=True)
-    saved_world = int(state.get("world_size", engine.world_size))
-    if saved_world != engine.world_size:
-        raise RuntimeError(
-            f"Checkpoint was saved with world_size={saved_world} but current "
-            f"world_size={engine.world_size}; ZeRO shards do not transfer."
-        )
-    if len(state["fp32_groups"]) != len(engine.flat_groups):
-        raise RuntimeError(
-            f"checkpoint has {len(state['fp32_groups'])} parameter groups, "
-            f"the engine {len(engine.flat_groups)}")
-    for g, buf in zip(engine.flat_groups, state["fp32_groups"]):
+def _restore_masters(engine, saved) -> None:
+    groups = engine.flat_groups
+    if len(saved) != len(groups):
+        raise RuntimeError(f"checkpoint has {len(saved)} parameter groups, the engine {len(groups)}")
+    for g, buf in zip(groups, saved):
         if buf.numel() != g.data.numel():
             raise RuntimeError(f"master buffer of {buf.numel()} elements, expected {g.data.numel()}")
         g.data.copy_(buf)
         g.copy_flat_to_model()
-    if engine.config.zero_stage >= 3:
-        engine.optimizer.free_parameters()
-        if was_gathered:
-            engine.optimizer.gather_parameters()
+
+
+@torch.no_grad()
+def save_checkpoint(engine, save_dir: str, tag: Optional[str] = None) -> str:
+    """Rank 0 writes the model state and ``latest``; every rank writes its
+    optimizer shard (checkpoint.py:35-71).  Returns the checkpoint folder."""
+    where = _Where(save_dir, tag or f"global_step{engine.global_steps}")
+    os.makedirs(where.folder, exist_ok=True)
+    with _full_parameters(engine):
+        if engine.rank == 0:
+            torch.save({"module": _to_host(engine.module.state_dict()), "tag": where.tag},
+                       where.model_file)
+            with open(os.path.join(save_dir, LATEST), "w", encoding="utf-8") as fh:
+                fh.write(where.tag)
+        torch.save(_shard_payload(engine), where.shard_file(engine.rank))
+        comm.barrier()
+    return where.folder
+
+
+@torch.no_grad()
+def load_checkpoint(engine, load_dir: str, tag: Optional[str] = None) -> Tuple[str, dict]:
+    """Model state, masters (cast into the parameters on the GPU), optimizer
+    shard, scheduler, scaler and counters (checkpoint.py:74-125).  Returns
+    ``(tag, the per-rank file's contents)``."""
+    where = _Where(load_dir, tag or read_latest(load_dir))
+    shard_file = where.shard_file(engine.rank)
+    with _full_parameters(engine, refresh=True):
+        model = torch.load(where.model_file, map_location="cpu", weights_only=True)
+        engine.module.load_state_dict(model["module"])
+        if not os.path.exists(shard_file):
+            raise FileNotFoundError(f"Missing optimizer shard for rank {engine.rank}: {shard_file}")
+        state = torch.load(shard_file, map_location="cpu", weights_only=True)
+        saved_world = int(state.get("world_size", engine.world_size))
+        if saved_world != engine.world_size:
+            raise RuntimeError(
+                f"Checkpoint was saved with world_size={saved_world} but current "
+                f"world_size={engine.world_size}; ZeRO shards do not transfer.")
+        _restore_masters(engine, state["fp32_groups"])
     engine.optimizer.load_state_dict(state["optimizer"])
     engine.lr_scheduler.load_state_dict(state["lr_scheduler"])
     engine.loss_scaler.load_state_dict(state["loss_scaler"])
-    engine.global_steps = int(state.get("global_steps", 0))
-    engine.micro_steps = int(state.get("micro_steps", 0))
-    engine.grad_norm = state.get("grad_norm")
+    for key, attr, cast in _COUNTERS:
+        value = state.get(key, 0 if cast else None)
+        setattr(engine, attr, cast(value) if cast else value)
     comm.barrier()
-    return tag, state
+    return where.tag, state

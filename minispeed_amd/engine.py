@@ -25,6 +25,7 @@ from typing import Iterable, Iterator, List, Optional, Union
 
 import torch
 from torch import nn
+from torch.utils._pytree import tree_map_only
 
 from . import _native, comm
 from . import checkpoint as ckpt
@@ -153,20 +154,17 @@ class DeepSpeedEngine:
 
     # ------------------------------------------------------------ nn surface
     def _cast_inputs(self, obj):
-        """Floating inputs follow the model dtype (engine.py:182-198)."""
-        if self._param_dtype is None:
+        """Floating-point tensors anywhere in ``obj`` (nested lists, tuples,
+        dicts) are cast to the model dtype; everything else passes through
+        (engine.py:182-198)."""
+        target = self._param_dtype
+        if target is None:
             return obj
-        if isinstance(obj, torch.Tensor):
-            if obj.is_floating_point() and obj.dtype != self._param_dtype:
-                return obj.to(self._param_dtype)
-            return obj
-        if isinstance(obj, dict):
-            return {k: self._cast_inputs(v) for k, v in obj.items()}
-        if isinstance(obj, tuple):
-            return tuple(self._cast_inputs(v) for v in obj)
-        if isinstance(obj, list):
-            return [self._cast_inputs(v) for v in obj]
-        return obj
+
+        def cast(t: torch.Tensor) -> torch.Tensor:
+            return t.to(target) if t.is_floating_point() else t
+
+        return tree_map_only(torch.Tensor, cast, obj)
 
     def forward(self, *args, **kwargs):
         if not self.optimizer.params_gathered:
@@ -223,8 +221,8 @@ class DeepSpeedEngine:
         if self.contiguous is not None:
             self.contiguous.next_window()
         overflow = bool(scalars.overflow)
+        self._check_device_scaler(scalars, self.loss_scaler.expected(overflow))
         self.loss_scaler.update(overflow=overflow)
-        self._check_device_scaler(scalars)
         if overflow:
             self.skipped_steps += 1
             self.optimizer.zero_grad()
@@ -242,17 +240,16 @@ class DeepSpeedEngine:
         self.global_steps += 1
         return True
 
-    def _check_device_scaler(self, scalars) -> None:
-        s = self.loss_scaler
-        if not s.enabled:
+    def _check_device_scaler(self, scalars, expected) -> None:
+        """K2 moved the loss-scale machine on the device; the host's
+        transition of the same state (``precision.scale_transition``) must
+        land on the same (scale, good_steps, skipped_steps)."""
+        if not self.loss_scaler.enabled:
             return
-        if (scalars.next_scale != s.scale or scalars.next_good_steps != s.good_steps
-                or scalars.next_skipped_steps != s.skipped_steps):
+        device = (scalars.next_scale, scalars.next_good_steps, scalars.next_skipped_steps)
+        if device != tuple(expected):
             raise RuntimeError(
-                "device loss-scale decision "
-                f"({scalars.next_scale}, {scalars.next_good_steps}, {scalars.next_skipped_steps}) "
-                f"differs from the host scaler ({s.scale}, {s.good_steps}, {s.skipped_steps})"
-            )
+                f"device loss-scale decision {device} differs from the host scaler's {tuple(expected)}")
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         if self.contiguous is not None:

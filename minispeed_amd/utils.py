@@ -1,11 +1,16 @@
-"""Named wall-clock timers and seeding (the ``engine.timers`` surface of
-minispeed/utils.py:14-66)."""
+"""``engine.timers`` and ``set_seed`` (the surface of minispeed/utils.py:14-66).
+
+Wall-clock sections on the host; they are what minispeed reports
+(``Timers.log()``: ``"name: 0.123s | ..."``).  Device time of the boundary
+kernels is measured with HIP events (``boundary.LaunchTimer``) and
+``rocprofv3``, not here: a host timer around an asynchronous launch sees
+only the launch, plus whatever host synchronisation the section contains.
+"""
 
 from __future__ import annotations
 
 import time
-from contextlib import contextmanager
-from typing import Dict, Iterator, List, Optional
+from typing import Dict, List
 
 import torch
 
@@ -13,49 +18,58 @@ from . import comm
 
 
 class Timer:
+    """Accumulated seconds of one named section; ``with timer.section():``
+    (or ``with timer:``) adds the wall time of the block."""
+
+    __slots__ = ("name", "elapsed", "_open")
+
     def __init__(self, name: str):
         self.name = name
         self.elapsed = 0.0
-        self.started_at: Optional[float] = None
+        self._open: List[float] = []    # start times of the sections entered, innermost last
 
-    @contextmanager
-    def section(self) -> Iterator[None]:
-        t0 = time.perf_counter()
-        try:
-            yield
-        finally:
-            self.elapsed += time.perf_counter() - t0
+    def __enter__(self) -> "Timer":
+        self._open.append(time.perf_counter())
+        return self
+
+    def __exit__(self, *exc) -> bool:
+        self.elapsed += time.perf_counter() - self._open.pop()
+        return False
+
+    def section(self) -> "Timer":
+        return self
 
     def reset(self) -> None:
         self.elapsed = 0.0
 
 
-class Timers:
-    def __init__(self) -> None:
-        self._timers: Dict[str, Timer] = {}
+class Timers(Dict[str, Timer]):
+    """Registry of named :class:`Timer`s, created on first use."""
+
+    def __missing__(self, name: str) -> Timer:
+        timer = self[name] = Timer(name)
+        return timer
 
     def __call__(self, name: str) -> Timer:
-        return self._timers.setdefault(name, Timer(name))
+        return self[name]
 
-    @contextmanager
-    def timer(self, name: str) -> Iterator[None]:
-        with self(name).section():
-            yield
+    def timer(self, name: str) -> Timer:
+        return self[name]
 
     def names(self) -> List[str]:
-        return list(self._timers)
+        return list(self.keys())
 
     def reset(self) -> None:
-        for t in self._timers.values():
-            t.reset()
+        for t in self.values():
+            t.elapsed = 0.0
 
     def log(self, rank0_only: bool = True) -> str:
+        """``"name: 0.123s | ..."`` in creation order; empty off rank 0."""
         if rank0_only and comm.get_rank() != 0:
             return ""
-        return " | ".join(f"{n}: {t.elapsed:.3f}s" for n, t in self._timers.items())
+        return " | ".join("%s: %.3fs" % (t.name, t.elapsed) for t in self.values())
 
 
 def set_seed(seed: int) -> None:
-    torch.manual_seed(seed)
-    if torch.cuda.is_available():
-        torch.cuda.manual_seed_all(seed)
+    """Seed torch's generators on the CPU and on every GPU."""
+    torch.manual_seed(int(seed))

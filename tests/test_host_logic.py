@@ -8,6 +8,7 @@ schedule KATs run against both this package and the oracle.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 from torch import nn
@@ -265,3 +266,39 @@ def test_timers_accumulate():
     assert "step:" in t.log()
     t.reset()
     assert t("step").elapsed == 0.0
+
+
+def test_scale_transition_equals_the_oracle_scaler_on_random_runs():
+    """The package's pure transition function and the oracle's scaler (the
+    reference's state machine restated, pinned by minispeed's own recorded
+    trajectories) walk the same (scale, good, skipped) path."""
+    from minispeed_amd.precision import ScaleState, scale_transition
+
+    rng = np.random.default_rng(3)
+    for trial in range(200):
+        window = int(rng.integers(1, 6))
+        start = float(2.0 ** int(rng.integers(0, 26)))
+        ref = ob.LossScaler(enabled=True, init_scale=start, scale_window=window)
+        state = ScaleState(start, 0, 0)
+        for overflow in rng.random(60) < rng.random():
+            ref.update(bool(overflow))
+            state = scale_transition(state, bool(overflow), window=window, min_scale=1.0,
+                                     max_scale=2.0 ** 24)
+            assert state == (ref.scale, ref.good_steps, ref.skipped_steps), trial
+
+
+def test_schedule_functions_equal_the_oracle_schedule_bit_for_bit():
+    from minispeed_amd.optim.scheduler import WarmupSpec, warmup_decay_lr, warmup_lr
+
+    rng = np.random.default_rng(4)
+    for trial in range(100):
+        lo, hi = sorted(float(x) for x in rng.random(2) * 1e-2)
+        warm = int(rng.integers(-2, 50))
+        total = None if trial % 7 == 0 else warm + int(rng.integers(-5, 200))
+        for kind, fn in (("WarmupLR", warmup_lr), ("WarmupDecayLR", warmup_decay_lr)):
+            groups = [{"lr": 0.0}]
+            ref = ob.Schedule(groups, kind, lo, hi, warm, total)
+            spec = WarmupSpec(lo, hi, max(0, warm), total)
+            for e in range(-1, 260):
+                ref.last_epoch = e
+                assert fn(spec, e) == ref.get_lr(), (trial, kind, e)
