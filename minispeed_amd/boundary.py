@@ -193,6 +193,7 @@ def run_boundary(
     materialize_flat_grad: bool,
     model_targets: Callable[[], List[Optional[List[int]]]],
     timer: Optional[LaunchTimer] = None,
+    keep: Sequence[Optional[torch.Tensor]] = (),
 ) -> _native.StepScalars:
     """Launch the whole boundary and return K2's scalars (one host sync).
 
@@ -203,9 +204,10 @@ def run_boundary(
     no write) is called after that, so whatever it does on the host overlaps
     K1 on the device.  The function returns once K2's scalars are on the
     host, which is before K3 has finished: K3 runs on the current stream, so
-    everything queued there afterwards is ordered after it.  The gradient
-    tensors behind ``GroupLaunch.grads`` may be dropped once this returns
-    (the caching allocator reuses their memory only in stream order).
+    everything queued there afterwards is ordered after it.  ``keep`` holds
+    the tensors behind ``GroupLaunch.grads``; the current stream is recorded
+    on each, so the caller may drop them once this returns, whichever
+    stream allocated them.
     """
     lib = _native.load()
     device = ws.device
@@ -280,6 +282,14 @@ def run_boundary(
         timer.stop(tok)
         _native.check(rc, "ms_fused_adamw")
 
+    # The gradients may come from another stream (the one backward ran on):
+    # once the caller drops them, the caching allocator could hand their
+    # memory to that stream while K1 / K3 still read it here.  Recording
+    # this stream on them defers the reuse until everything queued here so
+    # far has run.  Done while K1 / K2 run, before the host waits.
+    for t in keep:
+        if t is not None:
+            t.record_stream(cur)
     return ws.finish_readback()
 
 

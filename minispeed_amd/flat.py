@@ -196,13 +196,12 @@ class SegmentTable:
     through a fresh pinned host tensor with a non-blocking copy on the
     current stream, replacing the least recently used entry; torch's host
     allocator keeps the staging memory until the copy has run, and the copy
-    is stream-ordered before the kernels that read the table.  The copy
-    that overwrites a replaced entry is queued on the stream of the
-    boundary that uploads it, after every kernel of the earlier boundaries
-    that read the entry: the boundaries of one engine run on one stream, or
-    the new stream first waits for the old one (``Workspace.enter``).  Every
-    use records the current stream on the device table, so that when an
-    entry is dropped torch's caching allocator does not hand its memory to
+    is stream-ordered before the kernels that read the table.  A replaced
+    entry's device memory is overwritten in place only when every kernel
+    that read it ran on the uploading stream (the copy queues behind them);
+    otherwise the entry is dropped and a new one allocated.  Every use
+    records the current stream on the device table, so that when an entry
+    is dropped torch's caching allocator does not hand its memory to
     another stream before the kernels that read it have run.
     """
 
@@ -231,12 +230,17 @@ class SegmentTable:
                 return dev.data_ptr(), n
         staging = torch.empty((n, 4), dtype=torch.int64, pin_memory=True)
         staging.numpy()[:] = table
+        dev = None
         seen = set()
         if len(self._entries) >= self.SLOTS:
-            _, dev, seen = self._entries.pop(0)
-            if dev.shape[0] != n:
-                dev, seen = torch.empty((n, 4), dtype=torch.int64, device=self.device), set()
-        else:
+            _, old, old_seen = self._entries.pop(0)
+            # overwrite the evicted table in place only if every kernel that
+            # read it was queued on this stream (the copy is then ordered
+            # after them); a table another stream read is dropped instead,
+            # and record_stream keeps its memory until that stream is done
+            if old.shape[0] == n and old_seen <= {stream.cuda_stream}:
+                dev, seen = old, old_seen
+        if dev is None:
             dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
         dev.copy_(staging, non_blocking=True)
         if stream.cuda_stream not in seen:
@@ -619,42 +623,68 @@ class FlatParamGroup:
         """The owned range is the whole padded space (world size 1)."""
         return self.shard_start == 0 and self.shard_end == self.numel_padded
 
-    def _check_grad(self, g: torch.Tensor, n: int, dtype: torch.dtype) -> torch.Tensor:
+    def _check_grad(self, g: torch.Tensor, n: int) -> torch.Tensor:
         if g.numel() != n:
             raise RuntimeError(f"gradient of a parameter has {g.numel()} elements, expected {n}")
-        if g.dtype != dtype:
-            raise TypeError(f"gradient dtype {g.dtype} differs from parameter dtype {dtype}")
+        if g.dtype not in _ELEM_BYTES:
+            raise TypeError(f"gradient dtype {g.dtype} is not float32, float16 or bfloat16")
         if g.device != self.device:
             raise RuntimeError(f"gradient on {g.device}, expected {self.device}")
         return g.contiguous()
 
-    def grad_pointers(self) -> Tuple[np.ndarray, List[Optional[torch.Tensor]]]:
-        """Device address of every parameter's gradient (0: no gradient) and
+    def grad_pointers(self) -> Tuple[np.ndarray, List[Optional[torch.Tensor]], Optional[int]]:
+        """Device address of every parameter's gradient (0: no gradient),
         the tensors behind them, which the caller keeps alive until the
-        kernels reading them are queued.
+        kernels reading them are queued, and the ``MS_DTYPE_*`` the
+        addresses hold (``None``: the parameters' dtype).
 
         The addresses are an int64 array with one extra trailing 0 (the
-        padding row's).  Every gradient is checked against the first
-        parameter's dtype (the group's), its size, device and layout; the
-        C++ walk covers the common case and this loop takes over at the first
-        gradient it does not accept (to raise, or to make a contiguous copy).
+        padding row's).  Every gradient is checked for its size, device and
+        layout; the C++ walk covers the common case (every gradient in the
+        parameters' dtype) and this loop takes over at the first gradient it
+        does not accept, to raise, or to make a contiguous copy.  A gradient
+        in another floating dtype is widened like minispeed's flatten
+        (flat.py:209-212): then every gradient of the group is widened into
+        one fp32 buffer and the addresses point into it.
         """
         n_params = len(self.params)
         ptrs = np.zeros(n_params + 1, dtype=np.int64)
         bad, keep = _walk().grad_pointers(self.params, self._numels_np, self._device_index, ptrs)
-        if bad >= 0:
-            dtype = self.params[0].dtype
-            index = self._device_index
-            for k in range(bad, n_params):
-                g, n = self.params[k].grad, self._numels[k]
-                if g is not None:
-                    # dtypes are singletons; get_device() is -1 for host tensors
-                    if g.dtype is not dtype or g.numel() != n or g.get_device() != index \
-                            or not g.is_contiguous():
-                        g = self._check_grad(g, n, dtype)
-                    ptrs[k] = g.data_ptr()
-                keep.append(g)
-        return ptrs, keep
+        if bad < 0:
+            return ptrs, keep, None
+        dtype = self.params[0].dtype
+        index = self._device_index
+        mixed = False
+        for k in range(bad, n_params):
+            g, n = self.params[k].grad, self._numels[k]
+            if g is not None:
+                # dtypes are singletons; get_device() is -1 for host tensors
+                if g.dtype is not dtype or g.numel() != n or g.get_device() != index \
+                        or not g.is_contiguous():
+                    g = self._check_grad(g, n)
+                    mixed |= g.dtype is not dtype
+                ptrs[k] = g.data_ptr()
+            keep.append(g)
+        if not mixed:
+            return ptrs, keep, None
+        return self._widen_grads(keep)
+
+    def _widen_grads(self, grads: List[Optional[torch.Tensor]]):
+        """Every gradient widened exactly into its parameter's slice of one
+        fp32 buffer (the opt-in accumulation kernel with ``first`` set):
+        addresses into it, the tensors to keep, and ``MS_DTYPE_F32``."""
+        buf = torch.empty(self.numel, dtype=torch.float32, device=self.device)
+        base = buf.data_ptr()
+        ptrs = np.zeros(len(self.params) + 1, dtype=np.int64)
+        lib = _native.load()
+        stream = _native.stream_handle(self.device)
+        for k, (g, off, n) in enumerate(zip(grads, self.layout.offsets, self._numels)):
+            if g is None or n == 0:
+                continue
+            _native.check(lib.ms_accumulate_grad(base + 4 * off, g.data_ptr(), _native.ms_dtype(g.dtype),
+                                                 n, 1, stream), "ms_accumulate_grad(widen)")
+            ptrs[k] = base + 4 * off
+        return ptrs, [*grads, buf], _native.DTYPE_F32
 
     def model_pointers(self) -> np.ndarray:
         """Device address of every parameter's storage (the cast target),
@@ -716,30 +746,32 @@ class FlatParamGroup:
         return table
 
     # ----------------------------------------------------------- grads
-    def grad_storages(self) -> Tuple[List[Optional[tuple]], List[torch.Tensor]]:
+    def grad_storages(self) -> Tuple[List[Optional[tuple]], List[torch.Tensor], List[tuple]]:
         """Ragged gradient storage of every parameter, in group order.
 
-        Returns the storage descriptors and the tensors they point into (the
-        caller keeps those alive until the kernels reading them have run).
+        Returns the storage descriptors of the gradients in the group's
+        dtype (``None`` for the others), the tensors they point into (the
+        caller keeps those alive until the kernels reading them have run),
+        and ``(flat offset, numel, tensor)`` of every gradient in another
+        floating dtype.
         """
         stores: List[Optional[tuple]] = []
         keep: List[torch.Tensor] = []
+        foreign: List[tuple] = []
         dtype = self.model_dtype()
         for (offset, p), n in zip(self._offsets, self._numels):
             g = p.grad
             if g is None:
                 stores.append(None)
                 continue
-            if g.numel() != n:
-                raise RuntimeError(
-                    f"gradient of a parameter has {g.numel()} elements, expected {n}"
-                )
-            if g.dtype != dtype:
-                raise TypeError(f"gradient dtype {g.dtype} differs from parameter dtype {dtype}")
-            g = _flat_view(g.detach())
+            g = self._check_grad(g.detach(), n)
             keep.append(g)
-            stores.append(self._storage(g, (offset, offset + n)))
-        return stores, keep
+            if g.dtype == dtype:
+                stores.append(self._storage(g, (offset, offset + n)))
+            else:
+                stores.append(None)
+                foreign.append((offset, n, g))
+        return stores, keep, foreign
 
     def release_grads(self) -> None:
         for p in self.params:
@@ -748,21 +780,34 @@ class FlatParamGroup:
     @torch.no_grad()
     def flatten_grads(self) -> None:
         """``param.grad`` -> fp32 flat ``grad`` (flat.py:196-213); params
-        without a gradient contribute zeros, ``param.grad`` is released."""
+        without a gradient contribute zeros, every floating dtype is widened
+        exactly, ``param.grad`` is released."""
         if self.grad is None:
             self.grad = torch.empty(self.numel_padded, dtype=torch.float32, device=self.device)
-        stores, keep = self.grad_storages()
+        stores, keep, foreign = self.grad_storages()
         table = self.layout.segments(0, self.numel_padded, stores, [None] * len(stores))
         check_table(table, 0, self.numel_padded)
         ptr, n = self.table("flatten").upload(table)
-        rc = _native.load().ms_grad_stats(
+        lib = _native.load()
+        stream = _native.stream_handle(self.device)
+        rc = lib.ms_grad_stats(
             ptr, n, _native.ms_dtype(self.model_dtype()), 0, self.numel_padded, 0, 0, 0, 1.0,
-            self.grad.data_ptr(), None, None, 0, _native.stream_handle(self.device),
+            self.grad.data_ptr(), None, None, 0, stream,
         )
         _native.check(rc, "ms_grad_stats(flatten)")
+        # gradients of another dtype: their slices hold zeros now; widen them in
+        for off, numel, g in foreign:
+            _native.check(lib.ms_accumulate_grad(self.grad.data_ptr() + 4 * off, g.data_ptr(),
+                                                 _native.ms_dtype(g.dtype), numel, 1, stream),
+                          "ms_accumulate_grad(widen)")
         self._grad_dirty = True
         self.release_grads()
-        del keep  # stream order keeps the storage valid for the launched kernel
+        # the gradients may have been allocated on another stream: their
+        # memory must not be reused there before the kernel above has read it
+        cur = torch.cuda.current_stream(self.device)
+        for g in keep:
+            g.record_stream(cur)
+        del keep
 
     @torch.no_grad()
     def zero_grad(self) -> None:

@@ -136,7 +136,7 @@ class ZeROOptimizer:
             if self.contiguous is not None:
                 ptrs, grad_dtype = self.contiguous.grad_pointers(gi), _native.DTYPE_F32
             else:
-                ptrs, tensors = g.grad_pointers()
+                ptrs, tensors, grad_dtype = g.grad_pointers()
                 keep.extend(tensors)
             lr, betas, eps, wd = FlatAdam.hyper(group)
             launches.append(GroupLaunch(
@@ -155,9 +155,9 @@ class ZeROOptimizer:
         scalars = run_boundary(
             launches, ws, scaler=scaler, max_norm=max_norm,
             materialize_flat_grad=materialize_flat_grad, model_targets=model_targets,
-            timer=self.launch_timer,
+            timer=self.launch_timer, keep=keep,
         )
-        del keep  # K3 may still run: freed memory is reused in stream order
+        del keep  # recorded on the boundary's stream by run_boundary
         overflow = bool(scalars.overflow)
         if not overflow:
             self.grad_norm = float(scalars.norm)

@@ -349,6 +349,45 @@ def test_boundaries_on_alternating_streams_match_one_stream():
     assert results[0][2] == results[1][2]
 
 
+@pytest.mark.parametrize("materialize", [False, True])
+def test_gradients_from_another_stream_outlive_the_boundary_kernels(materialize):
+    """Gradients allocated on a producer stream, step() on a consumer
+    stream, then, with no wait, the producer allocates and fills tensors of
+    the same size: the caching allocator must not hand the gradients'
+    memory to the producer while K1 / K3 on the consumer still read it.
+    The run must equal the same steps taken on one stream."""
+    n = 1 << 25
+    cfg = {"train_micro_batch_size_per_gpu": 1, "gradient_accumulation_steps": 1,
+           "gradient_clipping": 1.0, "dtype": "fp16",
+           "fp16": {"enabled": True, "loss_scale": 0, "initial_scale_power": 16},
+           "optimizer": {"type": "AdamW", "params": {"lr": 1e-3, "weight_decay": 0.01}},
+           "hip_boundary": {"materialize_flat_grad": materialize}}
+    gen = torch.Generator().manual_seed(11)
+    host_grads = [(torch.randn(n, generator=gen) * 1e-3 * 2.0 ** 16).half() for _ in range(3)]
+    init = torch.randn(n, generator=gen) * 0.02
+    results = []
+    for split in (False, True):
+        p = nn.Parameter(init.clone().to(DEV))
+        engine = ms.initialize(model=nn.ParameterList([p]), model_parameters=[p], config=cfg)
+        producer, consumer = torch.cuda.Stream(), torch.cuda.Stream()
+        for hg in host_grads:
+            with torch.cuda.stream(producer):
+                p.grad = hg.to(DEV)                     # allocated on the producer stream
+            consumer.wait_stream(producer)
+            with torch.cuda.stream(consumer if split else producer):
+                engine.micro_steps += 1
+                assert engine.step() is True
+            with torch.cuda.stream(producer):           # no wait on the consumer
+                junk = torch.full((n,), float("nan"), dtype=torch.float16, device=DEV)
+                del junk
+        torch.cuda.synchronize()
+        results.append((engine.flat_groups[0].data.clone(),
+                        engine.optimizer.state[0]["exp_avg_sq"].clone(), engine.grad_norm))
+    assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])
+    assert results[0][2] == results[1][2]
+    assert torch.isfinite(results[1][0]).all()
+
+
 def test_thousands_of_tiny_tensors_against_the_oracle():
     """3000 parameters of 1..300 elements (segment tables of thousands of
     rows, most tiles straddling segment edges), fp16, ZeRO-2, clip: every

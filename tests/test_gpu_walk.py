@@ -28,7 +28,8 @@ def test_addresses_are_the_tensors_own():
     params, g = _group()
     for k, p in enumerate(params):
         p.grad = None if k == 3 else torch.randn_like(p)
-    ptrs, keep = g.grad_pointers()
+    ptrs, keep, gdt = g.grad_pointers()
+    assert gdt is None
     assert ptrs.dtype == np.int64 and ptrs.shape == (len(params) + 1,) and ptrs[-1] == 0
     for k, p in enumerate(params):
         if p.grad is None:
@@ -45,20 +46,36 @@ def test_non_contiguous_gradient_is_copied_and_the_rest_still_walked():
         p.grad = torch.randn_like(p)
     params[2].grad = torch.randn(4, 6, device=DEV, dtype=torch.float16).t()   # (6, 4) strided
     assert not params[2].grad.is_contiguous()
-    ptrs, keep = g.grad_pointers()
+    ptrs, keep, gdt = g.grad_pointers()
+    assert gdt is None
     assert keep[2].is_contiguous() and torch.equal(keep[2], params[2].grad)
     assert ptrs[2] == keep[2].data_ptr() != params[2].grad.data_ptr()
     for k in (0, 1, 3, 4, 5):
         assert ptrs[k] == params[k].grad.data_ptr() and keep[k] is params[k].grad
 
 
-def test_gradient_of_another_dtype_raises():
+def test_gradient_of_another_dtype_widens_the_group():
+    """minispeed's flatten copies any gradient dtype into the fp32 flat
+    buffer (flat.py:209-212): one fp32 gradient in an fp16 group makes the
+    walk widen every gradient of the group into one fp32 buffer."""
     params, g = _group()
-    for p in params:
-        p.grad = torch.randn_like(p)
-    params[4].data = params[4].data.float()
+    for k, p in enumerate(params):
+        p.grad = None if k == 3 else torch.randn_like(p)
     params[4].grad = torch.randn(129, device=DEV)
-    with pytest.raises(TypeError, match="dtype"):
+    ptrs, keep, gdt = g.grad_pointers()
+    assert gdt == 0                                    # MS_DTYPE_F32
+    buf = keep[-1]
+    assert buf.dtype == torch.float32 and buf.numel() == g.numel
+    torch.cuda.synchronize()
+    for k, p in enumerate(params):
+        off, n = g.layout.offsets[k], g.layout.numels[k]
+        if p.grad is None:
+            assert ptrs[k] == 0
+            continue
+        assert ptrs[k] == buf.data_ptr() + 4 * off
+        assert torch.equal(buf[off:off + n], p.grad.reshape(-1).float())
+    params[5].grad = torch.zeros(6, device=DEV, dtype=torch.float64)
+    with pytest.raises(TypeError, match="float64"):
         g.grad_pointers()
 
 
