@@ -29,7 +29,11 @@
 extern "C" {
 #endif
 
-#define MS_ABI_VERSION 3
+#define MS_ABI_VERSION 4
+
+/* groups one ms_boundary_scalars_noalloc call can scan (its static scratch:
+ * MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() partial slots of 12 bytes) */
+#define MS_SCRATCH_MAX_GROUPS 8
 
 /* element types of ragged gradient / model storage */
 enum {
@@ -53,7 +57,8 @@ enum {
   MS_OK = 0,
   MS_EINVAL = -1,   /* bad size, range, dtype or NULL where required */
   MS_ETABLE = -2,   /* segment count out of range */
-  MS_EBLOCKS = -3   /* partial-sum workspace smaller than ms_stats_blocks() */
+  MS_EBLOCKS = -3,  /* partial-sum workspace smaller than ms_stats_blocks() */
+  MS_ESCRATCH = -4  /* more groups than MS_SCRATCH_MAX_GROUPS */
 };
 
 /*
@@ -234,6 +239,42 @@ int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
  */
 int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n,
                        int32_t first, void* stream);
+
+/* One group's part of ms_boundary_scalars_noalloc: the arguments
+ * ms_grad_stats takes for it. */
+typedef struct ms_group_scan {
+  const ms_segment_t* segs; /* [dev] tiles [begin, end); may be NULL if empty */
+  int32_t nseg;
+  int32_t grad_dtype;       /* MS_DTYPE_* of segs[].grad */
+  int64_t begin, end;       /* scanned flat range (flag) */
+  int64_t own_begin, own_end; /* counted range (sum of squares) */
+} ms_group_scan_t;
+
+/*
+ * K1 over every group, then K2: the boundary's scalars with no workspace
+ * argument and no allocation.  No counterpart in minispeed; for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  Equals ms_grad_stats on each
+ * group (block_sumsq / block_flag of group g at slot g * ms_stats_blocks())
+ * followed by ms_norm_clip, bit for bit.
+ *
+ * groups [host]: ngroups entries, 0 <= ngroups <= MS_SCRATCH_MAX_GROUPS
+ *   (more: MS_ESCRATCH, nothing launched).  unscale / grad_scale apply to
+ *   every group as in ms_grad_stats; the clip, scaler, out and out_host
+ *   arguments are ms_norm_clip's.
+ * The partial sums live in a static device array of the library
+ * (MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() x 12 bytes = 1.5 MiB), one per
+ * GPU, held until the process ends; its address is looked up once per
+ * device on the first call there.  K1 writes every slot K2 reads, so nothing
+ * must be cleared between calls.  Calls that overlap on one GPU (two streams,
+ * or two threads) share that array and race: serialize them.
+ */
+int ms_boundary_scalars_noalloc(const ms_group_scan_t* groups, int32_t ngroups,
+                                int32_t unscale, float grad_scale, int32_t has_clip,
+                                double max_norm, int32_t scaler_enabled, double scale,
+                                int64_t good_steps, int64_t skipped_steps, int64_t window,
+                                double min_scale, double max_scale, ms_step_scalars_t* out,
+                                ms_step_scalars_t* out_host, void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,7 +19,7 @@ from typing import Optional
 import torch  # noqa: F401  (must precede the dlopen below, see module doc)
 
 LIB_NAME = "libminispeed_boundary.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -87,6 +87,20 @@ class AdamWParams(ctypes.Structure):
     ]
 
 
+class GroupScan(ctypes.Structure):
+    """``ms_group_scan_t``: one group of ms_boundary_scalars_noalloc."""
+
+    _fields_ = [
+        ("segs", ctypes.c_void_p),
+        ("nseg", ctypes.c_int32),
+        ("grad_dtype", ctypes.c_int32),
+        ("begin", ctypes.c_int64),
+        ("end", ctypes.c_int64),
+        ("own_begin", ctypes.c_int64),
+        ("own_end", ctypes.c_int64),
+    ]
+
+
 SEGMENT_BYTES = ctypes.sizeof(Segment)
 SCALARS_BYTES = ctypes.sizeof(StepScalars)
 
@@ -115,7 +129,15 @@ SIGNATURES = {
     ),
     "ms_cast_to_model": (ctypes.c_int, [_P, _I64, _I64, _P, _I32, _I32, _P]),
     "ms_accumulate_grad": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _P]),
+    "ms_boundary_scalars_noalloc": (
+        ctypes.c_int,
+        [ctypes.POINTER(GroupScan), _I32, _I32, _F, _I32, _D, _I32, _D, _I64, _I64, _I64, _D, _D,
+         _P, _P, _P],
+    ),
 }
+
+SCRATCH_MAX_GROUPS = 8
+ESCRATCH = -4
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

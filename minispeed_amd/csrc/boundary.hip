@@ -34,7 +34,18 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "minispeed_boundary.h"
+
+// Partial sums and flags of ms_boundary_scalars_noalloc: for each of
+// MS_SCRATCH_MAX_GROUPS groups kStatsBlocksFixed fp64 sums, then as many
+// uint32 flags.  Host code never names this array directly (its host-side
+// name is not a device address): it uses the per-device address from
+// hipGetSymbolAddress (scratch_base below).
+constexpr int kStatsBlocksFixed = 16384;
+static __device__ __align__(256) unsigned char scratch[MS_SCRATCH_MAX_GROUPS * kStatsBlocksFixed *
+                                                       (sizeof(double) + sizeof(uint32_t))];
 
 namespace {
 
@@ -48,7 +59,7 @@ constexpr int kTile = kThreads * kVec;    // 1024 flat elements
 // 512 threads take 8.09 / 8.16 / 8.00 / 8.11 ms for the 8B-param cast.
 constexpr int kCastThreads = 256;
 constexpr int kCastTile = kCastThreads * kVec;   // 2048 flat elements
-constexpr int kStatsBlocks = 16384;       // K1 partial slots per group
+constexpr int kStatsBlocks = kStatsBlocksFixed;   // K1 partial slots per group
 #ifndef MS_STATS_MIN_CHUNK
 #define MS_STATS_MIN_CHUNK 32768
 #endif
@@ -753,6 +764,71 @@ void launch_stats(const ms_segment_t* segs, int nseg, int64_t begin,
   }
 }
 
+// Host-side checks of one K1 scan (ms_grad_stats' arguments); MS_OK or the
+// error code, before anything is launched.
+int check_scan(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype, int64_t begin,
+               int64_t end, int32_t unscale, float grad_scale) {
+  if (!valid_dtype(grad_dtype) || begin < 0 || end < begin) return MS_EINVAL;
+  if (end > begin && (segs == nullptr || nseg <= 0)) return MS_ETABLE;
+  if (nseg < 0 || nseg > kMaxSegs) return MS_ETABLE;
+  if (unscale != MS_SCALE_NONE && unscale != MS_SCALE_DIVIDE && unscale != MS_SCALE_MULTIPLY)
+    return MS_EINVAL;
+  if (unscale == MS_SCALE_DIVIDE && !(grad_scale > 0.0f)) return MS_EINVAL;
+  return MS_OK;
+}
+
+void launch_scan(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype, int64_t begin,
+                 int64_t end, int64_t own_begin, int64_t own_end, int32_t unscale,
+                 float grad_scale, float* flat_grad, double* bsum, uint32_t* bflag,
+                 int32_t nblk, hipStream_t st) {
+  switch (grad_dtype) {
+    case MS_DTYPE_F32:
+      launch_stats<DF32>(segs, nseg, begin, end, own_begin, own_end, unscale, grad_scale,
+                         flat_grad, bsum, bflag, nblk, st);
+      break;
+    case MS_DTYPE_F16:
+      launch_stats<DF16>(segs, nseg, begin, end, own_begin, own_end, unscale, grad_scale,
+                         flat_grad, bsum, bflag, nblk, st);
+      break;
+    default:
+      launch_stats<DBF16>(segs, nseg, begin, end, own_begin, own_end, unscale, grad_scale,
+                          flat_grad, bsum, bflag, nblk, st);
+      break;
+  }
+}
+
+// Device address of `scratch` on the GPU that `st` belongs to (the current
+// GPU for the null stream), looked up with that GPU current on the first
+// call there and kept: every GPU holds its own copy of the array.
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+unsigned char* scratch_ptr[kMaxDevices] = {};
+
+int scratch_base(hipStream_t st, unsigned char** out) {
+  int dev = 0;
+  hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return MS_EINVAL;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return static_cast<int>(e);
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (p == nullptr) return MS_EINVAL;
+    scratch_ptr[dev] = static_cast<unsigned char*>(p);
+  }
+  *out = scratch_ptr[dev];
+  return MS_OK;
+}
+
 template <class G, class M>
 void launch_adamw(float* p, float* m, float* v, const float* fg,
                   const ms_segment_t* segs, int nseg, int64_t begin, int64_t end,
@@ -804,6 +880,9 @@ const char* ms_error_string(int code) {
       return "segment count out of range";
     case MS_EBLOCKS:
       return "partial-sum workspace smaller than ms_stats_blocks()";
+    case MS_ESCRATCH:
+      return "more groups than MS_SCRATCH_MAX_GROUPS (the static scratch of "
+             "ms_boundary_scalars_noalloc)";
     default:
       break;
   }
@@ -822,27 +901,49 @@ int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
   if ((block_sumsq == nullptr) != (block_flag == nullptr)) return MS_EINVAL;
   if (block_sumsq == nullptr && flat_grad == nullptr) return MS_EINVAL;
   if (block_sumsq != nullptr && nblk < kStatsBlocks) return MS_EBLOCKS;
-  if (end > begin && (segs == nullptr || nseg <= 0)) return MS_ETABLE;
-  if (nseg < 0 || nseg > kMaxSegs) return MS_ETABLE;
-  if (unscale != MS_SCALE_NONE && unscale != MS_SCALE_DIVIDE && unscale != MS_SCALE_MULTIPLY)
-    return MS_EINVAL;
-  if (unscale == MS_SCALE_DIVIDE && !(grad_scale > 0.0f)) return MS_EINVAL;
+  const int rc = check_scan(segs, nseg, grad_dtype, begin, end, unscale, grad_scale);
+  if (rc != MS_OK) return rc;
   if (block_sumsq == nullptr && end == begin) return MS_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (grad_dtype) {
-    case MS_DTYPE_F32:
-      launch_stats<DF32>(segs, nseg, begin, end, own_begin, own_end, unscale,
-                         grad_scale, flat_grad, block_sumsq, block_flag, nblk, st);
-      break;
-    case MS_DTYPE_F16:
-      launch_stats<DF16>(segs, nseg, begin, end, own_begin, own_end, unscale,
-                         grad_scale, flat_grad, block_sumsq, block_flag, nblk, st);
-      break;
-    default:
-      launch_stats<DBF16>(segs, nseg, begin, end, own_begin, own_end, unscale,
-                          grad_scale, flat_grad, block_sumsq, block_flag, nblk, st);
-      break;
+  launch_scan(segs, nseg, grad_dtype, begin, end, own_begin, own_end, unscale, grad_scale,
+              flat_grad, block_sumsq, block_flag, nblk, static_cast<hipStream_t>(stream));
+  return launch_status();
+}
+
+int ms_boundary_scalars_noalloc(const ms_group_scan_t* groups, int32_t ngroups,
+                                int32_t unscale, float grad_scale, int32_t has_clip,
+                                double max_norm, int32_t scaler_enabled, double scale,
+                                int64_t good_steps, int64_t skipped_steps, int64_t window,
+                                double min_scale, double max_scale, ms_step_scalars_t* out,
+                                ms_step_scalars_t* out_host, void* stream) {
+  if (ngroups < 0 || (ngroups > 0 && groups == nullptr) || out == nullptr || window < 1)
+    return MS_EINVAL;
+  if (ngroups > MS_SCRATCH_MAX_GROUPS) return MS_ESCRATCH;
+  for (int g = 0; g < ngroups; ++g) {
+    const ms_group_scan_t& gs = groups[g];
+    const int rc = check_scan(gs.segs, gs.nseg, gs.grad_dtype, gs.begin, gs.end, unscale,
+                              grad_scale);
+    if (rc != MS_OK) return rc;
   }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned char* base = nullptr;
+  const int rc = scratch_base(st, &base);
+  if (rc != MS_OK) return rc;
+  double* sums = reinterpret_cast<double*>(base);
+  uint32_t* flags = reinterpret_cast<uint32_t*>(
+      base + sizeof(double) * MS_SCRATCH_MAX_GROUPS * kStatsBlocks);
+  for (int g = 0; g < ngroups; ++g) {
+    const ms_group_scan_t& gs = groups[g];
+    // every one of the group's kStatsBlocks slots is written (zeros after
+    // the last block), so the array needs no clearing between calls
+    launch_scan(gs.segs, gs.nseg, gs.grad_dtype, gs.begin, gs.end, gs.own_begin, gs.own_end,
+                unscale, grad_scale, nullptr, sums + static_cast<int64_t>(g) * kStatsBlocks,
+                flags + static_cast<int64_t>(g) * kStatsBlocks, kStatsBlocks, st);
+    const int lrc = launch_status();
+    if (lrc != MS_OK) return lrc;
+  }
+  hipLaunchKernelGGL(k_norm_clip, dim3(1), dim3(kNormThreads), 0, st, sums, flags, kStatsBlocks,
+                     ngroups, has_clip, max_norm, scaler_enabled, scale, good_steps,
+                     skipped_steps, window, min_scale, max_scale, out, out_host);
   return launch_status();
 }
 

@@ -60,6 +60,12 @@ int main(void) {
   printf("ms_adamw_params_t %zu\n", sizeof(ms_adamw_params_t));
   F(ms_adamw_params_t, neg_lr) F(ms_adamw_params_t, bias_c2) F(ms_adamw_params_t, grad_scale)
   F(ms_adamw_params_t, decay) F(ms_adamw_params_t, unscale)
+  printf("ms_group_scan_t %zu\n", sizeof(ms_group_scan_t));
+  F(ms_group_scan_t, segs) F(ms_group_scan_t, nseg) F(ms_group_scan_t, grad_dtype)
+  F(ms_group_scan_t, begin) F(ms_group_scan_t, end) F(ms_group_scan_t, own_begin)
+  F(ms_group_scan_t, own_end)
+  printf("MS_SCRATCH_MAX_GROUPS %d\n", MS_SCRATCH_MAX_GROUPS);
+  printf("MS_ESCRATCH %d\n", MS_ESCRATCH);
   return 0;
 }
 ''')
@@ -68,7 +74,9 @@ int main(void) {
     lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
     got = dict(line.rsplit(" ", 1) for line in lines if line)
     classes = {"ms_segment_t": _native.Segment, "ms_step_scalars_t": _native.StepScalars,
-               "ms_adamw_params_t": _native.AdamWParams}
+               "ms_adamw_params_t": _native.AdamWParams, "ms_group_scan_t": _native.GroupScan}
+    assert int(got.pop("MS_SCRATCH_MAX_GROUPS")) == _native.SCRATCH_MAX_GROUPS
+    assert int(got.pop("MS_ESCRATCH")) == _native.ESCRATCH
     for key, value in got.items():
         if "." in key:
             cname, field = key.split(".")
@@ -112,7 +120,19 @@ def test_host_argument_errors_return_codes_without_launching():
     assert lib.ms_cast_to_model(8, 0, 10, None, 0, 1, None) == ETABLE
     assert lib.ms_cast_to_model(8, 0, 10, 8, 1, 5, None) == EINVAL
     assert lib.ms_cast_to_model(None, 3, 3, None, 0, 1, None) == 0
-    for code in (0, EINVAL, ETABLE, EBLOCKS):
+    # the no-allocation boundary scan: group count beyond its scratch, bad
+    # arguments, and a bad group, all refused before any device call
+    scans = (_native.GroupScan * 9)()
+    noalloc = lib.ms_boundary_scalars_noalloc
+    assert noalloc(scans, 9, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == _native.ESCRATCH
+    assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, None, None, None) == EINVAL
+    assert noalloc(None, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == EINVAL
+    assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 0, 1.0, 1.0, 8, None, None) == EINVAL
+    scans[0] = _native.GroupScan(None, 0, 7, 0, 10, 0, 10)
+    assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == EINVAL
+    scans[0] = _native.GroupScan(None, 0, 1, 0, 10, 0, 10)
+    assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == ETABLE
+    for code in (0, EINVAL, ETABLE, EBLOCKS, _native.ESCRATCH):
         assert lib.ms_error_string(code)
     with pytest.raises(RuntimeError, match="segment count"):
         _native.check(ETABLE, "probe")
