@@ -357,12 +357,22 @@ class Engine:
             for g in self.groups:
                 g.grad = None
 
-    def clip_gradients(self, max_norm):                                   # stage_1_and_2.py:105-128
+    def clip_gradients(self, max_norm, clip_override=None):               # stage_1_and_2.py:105-128
+        """``clip_override`` = (applied, coefficient as a double) replaces
+        the clip decision and coefficient derived from this norm, so that a
+        test can run the AdamW arithmetic on exactly the gradients another
+        implementation clipped (the norm itself is still this one)."""
         local = torch.zeros((), dtype=torch.float32)
         for g in self.groups:
             local += g.local_grad_sumsq()
         norm = float(local.sqrt().item())
         self.grad_norm_raw = local
+        if clip_override is not None:
+            applied, coef = clip_override
+            if applied:
+                for g in self.groups:
+                    g.scale_grads(float(coef))
+            return norm
         if max_norm is not None and norm > max_norm:
             coef = max_norm / (norm + 1e-6)
             for g in self.groups:
@@ -377,11 +387,12 @@ class Engine:
                 g.copy_flat_to_model()
 
     @torch.no_grad()
-    def take_step(self, flat_grads=None) -> bool:                         # engine.py:268-322
+    def take_step(self, flat_grads=None, clip_override=None) -> bool:     # engine.py:268-322
         """``flat_grads`` (one fp32 flat tensor per group, numel_padded)
         stands in for the flatten of ``param.grad``: the boundary of the
         opt-in contiguous-gradient mode, which minispeed does not have; every
-        later step is the reference's."""
+        later step is the reference's.  ``clip_override``: see
+        :meth:`clip_gradients`."""
         if flat_grads is None:
             for g in self.groups:
                 g.flatten_grads()
@@ -402,7 +413,7 @@ class Engine:
             for g in self.groups:
                 g.unscale_grads(scale)
         self.reduce_gradients()
-        self.grad_norm = self.clip_gradients(self.clip)
+        self.grad_norm = self.clip_gradients(self.clip, clip_override)
         for group, g, st in zip(self.param_groups, self.groups, self.state):   # adam.py:59-93
             st["step"] += 1
             lr = float(group["lr"])
@@ -436,13 +447,13 @@ class Engine:
             if not g.partitioned:
                 g.copy_flat_to_model()
 
-    def step(self, flat_grads=None) -> bool:                              # engine.py:254-266
+    def step(self, flat_grads=None, clip_override=None) -> bool:          # engine.py:254-266
         if not (self.micro_steps > 0 and self.micro_steps % self.gas == 0):
             return False
         if getattr(self, "_consumed", -1) == self.micro_steps:
             return False
         self._consumed = self.micro_steps
-        return self.take_step(flat_grads)
+        return self.take_step(flat_grads, clip_override)
 
 
 def accumulate_fp32(acc: Optional[torch.Tensor], grad: torch.Tensor) -> torch.Tensor:

@@ -13,9 +13,12 @@ and the LR schedules.  Gradients are written straight into ``param.grad``
 between boundaries (the engine's micro-step counter is advanced as
 ``backward`` would), so every input of every boundary is recorded exactly.
 
-Two engine-level traces (an MLP trained through autograd, fp32 and bf16,
-gas 2) record losses and parameters; they pin the host-side loss scaling and
-boundary gating as well.  A third runs the tiny decoder LM of
+Three engine-level traces (an MLP trained through autograd: fp32 and bf16 at
+gas 2, fp16 with a dynamic loss scale starting at 2^20 and window 2 at gas 3)
+record losses, every boundary's outcome (applied or skipped, loss-scale
+state, grad_norm, lr) and the final parameters; they pin the host-side loss
+scaling of ``backward`` (loss * scale / gas), the accumulation of
+micro-batch gradients in the parameter dtype and the boundary gating.  A third runs the tiny decoder LM of
 ``tests/tinylm.py`` (3.3M parameters, fp32, ZeRO 0, 20 steps) and records
 its losses, gradient norms and per-tensor parameter sums (``cases.json`` key
 ``tinylm``): an end-to-end trace through autograd, compared on the GPU at a
@@ -202,7 +205,7 @@ class MLP(nn.Module):
         return self.net(x)
 
 
-def run_mlp_trace(ms, name, dtype, out_arrays, meta, steps=4, gas=2, micro=4):
+def run_mlp_trace(ms, name, dtype, out_arrays, meta, steps=4, gas=2, micro=4, fp16=None):
     torch.manual_seed(1234)
     model = MLP()
     for i, p in enumerate(model.parameters()):
@@ -215,22 +218,29 @@ def run_mlp_trace(ms, name, dtype, out_arrays, meta, steps=4, gas=2, micro=4):
     cfg = base_cfg(dtype, 0, 1.0, scheduler="WarmupDecayLR",
                    sched_params={"warmup_min_lr": 0.0, "warmup_max_lr": 1e-2,
                                  "warmup_num_steps": 1, "total_num_steps": 6},
-                   lr=1e-2, gas=gas)
+                   lr=1e-2, gas=gas, fp16=fp16)
     cfg["train_micro_batch_size_per_gpu"] = micro
     engine = ms.initialize(model=model, model_parameters=list(model.parameters()), config=cfg)
-    losses = []
+    losses, boundaries = [], []
     for s in range(steps):
         for mi in range(gas):
             loss = F.mse_loss(engine(x[s, mi]).float(), y[s, mi].float())
             losses.append(float(loss.detach()))
             engine.backward(loss)
-            engine.step()
+            applied = engine.step()
+            if engine.is_gradient_accumulation_boundary:
+                sc = engine.loss_scaler
+                boundaries.append({"applied": bool(applied), "scale": sc.scale,
+                                   "good_steps": sc.good_steps, "skipped_steps": sc.skipped_steps,
+                                   "grad_norm": engine.grad_norm,
+                                   "lr": [g["lr"] for g in engine.optimizer.param_groups],
+                                   "global_steps": engine.global_steps})
     for i, p in enumerate(model.parameters()):
         out_arrays[f"final_p{i}"] = bits(p.data)
     out_arrays["final_master0"] = engine.flat_groups[0].data.numpy().copy()
     meta[name] = {"config": cfg, "steps": steps, "gas": gas, "micro": micro,
                   "losses": losses, "grad_norm": engine.grad_norm,
-                  "global_steps": engine.global_steps}
+                  "global_steps": engine.global_steps, "boundaries": boundaries}
 
 
 def run_tinylm_trace(ms, meta, steps=20):
@@ -294,6 +304,12 @@ def main(argv=None):
         arrays = {}
         run_mlp_trace(ms, name, dtype, arrays, meta["cases"])
         save_npz(name, arrays)
+    # fp16 with a dynamic scale and gas 3: the loss is multiplied by
+    # scale / 3, a factor that rounds, and the first boundaries overflow
+    arrays = {}
+    run_mlp_trace(ms, "mlp_fp16_trace", "fp16", arrays, meta["cases"], steps=10, gas=3,
+                  fp16={"loss_scale": 0, "initial_scale_power": 20, "loss_scale_window": 2})
+    save_npz("mlp_fp16_trace", arrays)
     run_tinylm_trace(ms, meta)
     with open(os.path.join(HERE, "cases.json"), "w", encoding="utf-8") as fh:
         json.dump(meta, fh, indent=1, sort_keys=True)

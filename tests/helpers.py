@@ -155,3 +155,28 @@ def master_step_within_ulps(before, got, want, ulps=2.0):
     ratio = diff / np.spacing(scale).astype(np.float64)
     worst = float(ratio.max()) if ratio.size else 0.0
     return worst <= ulps, worst
+
+
+def clip_override(engine):
+    """The GPU boundary's clip decision and coefficient, for the oracle's
+    ``step(clip_override=...)``: the oracle then runs its AdamW arithmetic on
+    exactly the gradients the GPU clipped, so moments must match bit for bit
+    and masters within 2 fp32 ulp per step (the norm is checked on its own,
+    to 1e-5)."""
+    lb = engine.last_boundary
+    return bool(lb.clip_applied), float(lb.coef64)
+
+
+def relative_within(got, want, scale, rtol=1e-5):
+    """Per element |got - want| <= rtol * max(|want|, scale), with ``scale``
+    the element's largest magnitude along its trajectory: relative to the
+    element's own size, also where it passes near zero on the way.  Returns
+    (ok, worst ratio of the difference to its bound)."""
+    got = np.asarray(got, dtype=np.float32).astype(np.float64)
+    want64 = np.asarray(want, dtype=np.float32).astype(np.float64)
+    size = np.maximum(np.abs(want64), np.abs(np.asarray(scale, dtype=np.float32)).astype(np.float64))
+    diff = np.abs(got - want64)
+    bound = rtol * size
+    ratio = np.where(diff == 0.0, 0.0, diff / np.maximum(bound, np.finfo(np.float64).tiny))
+    worst = float(ratio.max()) if ratio.size else 0.0
+    return worst <= 1.0, worst

@@ -61,6 +61,8 @@ def test_gradient_of_another_dtype_widens_the_group():
     params, g = _group()
     for k, p in enumerate(params):
         p.grad = None if k == 3 else torch.randn_like(p)
+    if hasattr(params[4], "grad_dtype"):
+        params[4].grad_dtype = None      # torch >= 2.10 checks .grad's dtype unless told not to
     params[4].grad = torch.randn(129, device=DEV)
     ptrs, keep, gdt = g.grad_pointers()
     assert gdt == 0                                    # MS_DTYPE_F32
@@ -74,7 +76,9 @@ def test_gradient_of_another_dtype_widens_the_group():
             continue
         assert ptrs[k] == buf.data_ptr() + 4 * off
         assert torch.equal(buf[off:off + n], p.grad.reshape(-1).float())
-    params[5].grad = torch.zeros(6, device=DEV, dtype=torch.float64)
+    if hasattr(params[5], "grad_dtype"):
+        params[5].grad_dtype = None
+    params[5].grad = torch.zeros(2, 3, device=DEV, dtype=torch.float64)
     with pytest.raises(TypeError, match="float64"):
         g.grad_pointers()
 

@@ -83,23 +83,35 @@ def test_oracle_matches_reference_mlp_trace(name):
                 p.copy_(torch.from_numpy(arr[f"init_p{i}"]))
         opts = dict(cfg["optimizer"]["params"])
         opts["betas"] = tuple(opts["betas"])
+        fp16 = cfg.get("fp16", {})
         eng = ob.Engine([list(model.parameters())], [opts], dtype=cfg["dtype"], zero_stage=0,
                         clip=cfg["gradient_clipping"], gas=case["gas"],
+                        loss_scale=float(fp16.get("loss_scale", 0.0)),
+                        initial_scale_power=int(fp16.get("initial_scale_power", 16)),
+                        loss_scale_window=int(fp16.get("loss_scale_window", 1000)),
                         scheduler=cfg["scheduler"]["type"], scheduler_params=scheduler_params(cfg))
         x = torch.from_numpy(arr["x"])
         y = torch.from_numpy(arr["y"])
         dt = DTYPES[cfg["dtype"]]
-        losses = []
+        losses, boundaries = [], []
         for s in range(case["steps"]):
             for mi in range(case["gas"]):
                 xb = x[s, mi] if dt == torch.float32 else x[s, mi].to(dt)   # engine.py:182-198
                 loss = F.mse_loss(model(xb).float(), y[s, mi].float())
                 losses.append(float(loss.detach()))
                 eng.backward(loss)
-                eng.step()
+                applied = eng.step()
+                if eng.micro_steps % eng.gas == 0:
+                    sc = eng.scaler
+                    boundaries.append({"applied": bool(applied), "scale": sc.scale,
+                                       "good_steps": sc.good_steps, "skipped_steps": sc.skipped_steps,
+                                       "grad_norm": eng.grad_norm,
+                                       "lr": [g["lr"] for g in eng.param_groups],
+                                       "global_steps": eng.global_steps})
     finally:
         torch.set_num_threads(threads)
     assert losses == case["losses"]
+    assert boundaries == case["boundaries"]
     assert eng.grad_norm == case["grad_norm"]
     assert eng.global_steps == case["global_steps"]
     for i, p in enumerate(model.parameters()):
@@ -193,7 +205,7 @@ def test_golden_vectors_catch_planted_clip_and_scale_mistakes(monkeypatch):
     # clip on >= instead of > is invisible here; dropping the +1e-6 is not
     orig = ob.Engine.clip_gradients
 
-    def no_eps(self, max_norm):
+    def no_eps(self, max_norm, clip_override=None):
         local = torch.zeros((), dtype=torch.float32)
         for g in self.groups:
             local += g.local_grad_sumsq()
@@ -221,3 +233,48 @@ def test_golden_vectors_catch_planted_clip_and_scale_mistakes(monkeypatch):
 
     monkeypatch.setattr(ob.LossScaler, "update", update_no_reset)
     assert not _replays_cleanly("fp16_z2_clip")
+
+
+@pytest.mark.parametrize("name", ["fp16_z2_clip", "fp32_z0_clip_adam", "bf16_z1_noclip_2groups"])
+def test_clip_override_with_the_own_decision_replays_the_reference(name):
+    """The oracle's clip override (used by GPU tests to run the AdamW
+    arithmetic on the GPU's own clip coefficient) reproduces minispeed's
+    recorded trajectory when handed the decision the oracle itself makes."""
+    case = META["cases"][name]
+    arr = arrays(name)
+    eng, params = _oracle_engine(case, arr)
+    probe, probe_params = _oracle_engine(case, arr)
+    dtype = DTYPES[case["config"]["dtype"]]
+    stage = case["config"]["zero_optimization"]["stage"]
+    clip = case["config"].get("gradient_clipping")
+    for step, rec in enumerate(case["trajectory"]):
+        grads = case_grads(case, arr, step, dtype)
+        for ps, e in ((params, eng), (probe_params, probe)):
+            if stage >= 3:
+                e.gather_parameters()
+            for p, g in zip(ps, grads):
+                p.grad = None if g is None else g.clone()
+            e.micro_steps += 1
+        probe.step()                                   # the oracle's own decision
+        norm = probe.grad_norm
+        applied = bool(clip) and norm is not None and norm > clip
+        override = (applied, clip / (norm + 1e-6) if applied else 1.0)
+        assert eng.step(clip_override=override) == rec["applied"], step
+        for gi, g in enumerate(eng.groups):
+            np.testing.assert_array_equal(g.data.numpy(), arr[f"s{step}_master{gi}"])
+            np.testing.assert_array_equal(eng.state[gi]["exp_avg"].numpy(), arr[f"s{step}_m{gi}"])
+            np.testing.assert_array_equal(eng.state[gi]["exp_avg_sq"].numpy(), arr[f"s{step}_v{gi}"])
+
+
+def test_mlp_traces_catch_a_planted_loss_scaling_mistake(monkeypatch):
+    """The traces pin ``_scale_loss``: an oracle that forgets the division by
+    gas, or scales by a different factor, no longer reproduces them."""
+    def no_gas(self, loss):
+        factor = self.scaler.loss_scale_factor
+        return loss if factor == 1.0 else loss * factor
+
+    for mutant in (no_gas,):
+        monkeypatch.setattr(ob.Engine, "scale_loss", mutant)
+        for name in ("mlp_fp32_trace", "mlp_fp16_trace"):
+            with pytest.raises(AssertionError):
+                test_oracle_matches_reference_mlp_trace(name)
