@@ -17,11 +17,12 @@
 //                     into its flat slice (contiguous gradients)
 //
 // Everything here is HBM-bound streaming; no MFMA.  Work is cut into tiles
-// of kTile consecutive flat indices; a lane owns kVec consecutive elements
-// of a tile.  A tile that lies inside one segment with 16-byte aligned
-// storage takes the vector path (dwordx4 loads/stores on every stream);
-// tiles that straddle segment edges, partial tail tiles and misaligned
-// segments take the per-element path.
+// of consecutive flat indices.  In K3 and K4 a lane moves quads of 4
+// elements in wave order (see kStreamThreads); in K1 and K5 it owns groups
+// of kVec consecutive elements.  A tile (K3-K5) or a segment piece (K1) with
+// suitably aligned storage takes the vector path; tiles that straddle
+// segment edges, partial tail tiles and misaligned segments take a
+// per-element path.
 //
 // Arithmetic is written so that each rounding point of minispeed's torch op
 // sequence is one IEEE fp32 operation here: the file is compiled with
@@ -49,16 +50,28 @@ static __device__ __align__(256) unsigned char scratch[MS_SCRATCH_MAX_GROUPS * k
 
 namespace {
 
-// Streaming kernels (K3-K5): 2 wave64 per block, one 1024-element tile per
-// block.  Measured on the 1.3B AdamW step: 64 / 128 / 256 / 512 / 1024
-// threads per block take 6.69 / 6.65 / 6.78 / 6.83 / 6.87 ms.
+// K5: 2 wave64 per block, kVec consecutive elements per lane, one
+// 1024-element tile per block.
 constexpr int kThreads = 128;
-constexpr int kVec = 8;                   // elements per lane per tile
+constexpr int kVec = 8;                   // elements per lane per tile (K1, K5)
 constexpr int kTile = kThreads * kVec;    // 1024 flat elements
-// K4 (2 B read : 1 B written) prefers 4 wave64 per block: 64 / 128 / 256 /
-// 512 threads take 8.09 / 8.16 / 8.00 / 8.11 ms for the 8B-param cast.
-constexpr int kCastThreads = 256;
-constexpr int kCastTile = kCastThreads * kVec;   // 2048 flat elements
+
+// K3 and K4 stream in "wave" order: a tile is kStreamThreads x kStreamUnroll
+// quads of 4 consecutive elements, and quad u of lane j is quad
+// u * kStreamThreads + j, so every load or store instruction of a wave
+// covers one contiguous run (64 x 16 bytes of fp32) and every cache line it
+// touches is whole.  That is what lets every stream carry the non-temporal
+// hint: with 8 consecutive elements per lane a store instruction writes
+// half lines, and non-temporal half-line writes cost the fused AdamW ~40%.
+#ifndef MS_STREAM_THREADS
+#define MS_STREAM_THREADS 256
+#endif
+#ifndef MS_STREAM_UNROLL
+#define MS_STREAM_UNROLL 2
+#endif
+constexpr int kStreamThreads = MS_STREAM_THREADS;
+constexpr int kStreamUnroll = MS_STREAM_UNROLL;
+constexpr int kStreamTile = kStreamThreads * kStreamUnroll * 4;   // 2048 flat elements
 constexpr int kStatsBlocks = kStatsBlocksFixed;   // K1 partial slots per group
 #ifndef MS_STATS_MIN_CHUNK
 #define MS_STATS_MIN_CHUNK 32768
@@ -68,7 +81,14 @@ constexpr int kStatsBlocks = kStatsBlocksFixed;   // K1 partial slots per group
 // function of n, so the partition (and the norm's bits) never varies run
 // to run, and small groups do not pay for 16384 mostly idle blocks.
 constexpr int64_t kStatsMinChunk = MS_STATS_MIN_CHUNK;
-constexpr int kScanThreads = 512;         // K1 block: 8 wave64
+#ifndef MS_SCAN_THREADS
+#define MS_SCAN_THREADS 512
+#endif
+constexpr int kScanThreads = MS_SCAN_THREADS;   // K1 block: 8 wave64
+#ifndef MS_SCAN_DEPTH
+#define MS_SCAN_DEPTH 4
+#endif
+constexpr int kScanDepth = MS_SCAN_DEPTH;   // K1 vector groups in flight per lane
 constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
 constexpr int kMaxSegs = 1 << 26;
 
@@ -127,11 +147,8 @@ struct DBF16 {
   }
 };
 
-// Load / store kVec consecutive raw elements at a 16-byte aligned address.
-// These move the streams the boundary touches exactly once (the ragged
-// gradients in K3, the model-dtype copy in K3/K4), so they carry the
-// non-temporal hint; the fp32 masters and moments, read and then written
-// back, do not (measured: hinting those costs ~30% of K3's bandwidth).
+// Load / store kVec consecutive raw elements at a 16-byte aligned address
+// (K5's per-parameter gradient reads), with the non-temporal hint.
 template <class D>
 __device__ inline void load_raw8(const void* p, typename D::raw (&r)[kVec]) {
   if constexpr (D::kBytes == 2) {
@@ -152,13 +169,14 @@ __device__ inline void load_raw8(const void* p, typename D::raw (&r)[kVec]) {
   }
 }
 
-// kVec raw elements as 32-bit words (kVec*kBytes/4 of them), 16-byte aligned.
+// kVec raw elements as 32-bit words (kVec*kBytes/4 of them), 16-byte aligned,
+// with the non-temporal hint (K1 reads each gradient once).
 template <class D>
 __device__ inline void load_words(const void* p, uint32_t (&w)[kVec * D::kBytes / 4]) {
   const u4* q = reinterpret_cast<const u4*>(p);
 #pragma unroll
   for (int j = 0; j < kVec * D::kBytes / 16; ++j) {
-    const u4 x = q[j];
+    const u4 x = __builtin_nontemporal_load(q + j);
 #pragma unroll
     for (int k = 0; k < 4; ++k) w[4 * j + k] = x[k];
   }
@@ -170,28 +188,6 @@ __device__ inline typename D::raw word_elem(const uint32_t (&w)[kVec * D::kBytes
     return static_cast<uint16_t>((k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu));
   else
     return w[k];
-}
-
-template <class D>
-__device__ inline void store_raw8(void* p, const typename D::raw (&r)[kVec]) {
-  if constexpr (D::kBytes == 2) {
-    u4 w;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      w[k] = static_cast<uint32_t>(r[2 * k]) |
-             (static_cast<uint32_t>(r[2 * k + 1]) << 16);
-    __builtin_nontemporal_store(w, reinterpret_cast<u4*>(p));
-  } else {
-    u4* q = reinterpret_cast<u4*>(p);
-    u4 a, b;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      a[k] = r[k];
-      b[k] = r[4 + k];
-    }
-    __builtin_nontemporal_store(a, q);
-    __builtin_nontemporal_store(b, q + 1);
-  }
 }
 
 __device__ inline void load_f8(const float* p, float (&x)[kVec]) {
@@ -214,6 +210,55 @@ __device__ inline void store_f8(float* p, const float (&x)[kVec]) {
   }
   q[0] = a;
   q[1] = b;
+}
+
+// A quad: 4 consecutive elements, 16 bytes of fp32 or 8 of fp16 / bf16, at an
+// address aligned to its size.  Every K3 / K4 stream is touched once per
+// element (read, then written back once) and moves through these with the
+// non-temporal hint.
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+__device__ inline void ldq(const float* p, float (&x)[4]) {
+  const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+  x[0] = v[0];
+  x[1] = v[1];
+  x[2] = v[2];
+  x[3] = v[3];
+}
+
+__device__ inline void stq(float* p, const float (&x)[4]) {
+  __builtin_nontemporal_store(f4{x[0], x[1], x[2], x[3]}, reinterpret_cast<f4*>(p));
+}
+
+template <class D>
+__device__ inline void ldq_raw(const void* p, float (&x)[4]) {
+  if constexpr (D::kBytes == 2) {
+    const u2 w = __builtin_nontemporal_load(reinterpret_cast<const u2*>(p));
+    x[0] = D::widen(static_cast<uint16_t>(w[0] & 0xffffu));
+    x[1] = D::widen(static_cast<uint16_t>(w[0] >> 16));
+    x[2] = D::widen(static_cast<uint16_t>(w[1] & 0xffffu));
+    x[3] = D::widen(static_cast<uint16_t>(w[1] >> 16));
+  } else {
+    ldq(static_cast<const float*>(p), x);
+  }
+}
+
+template <class D>
+__device__ inline void stq_raw(void* p, const float (&x)[4]) {
+  if constexpr (D::kBytes == 2) {
+    u2 w;
+    w[0] = static_cast<uint32_t>(D::narrow(x[0])) | (static_cast<uint32_t>(D::narrow(x[1])) << 16);
+    w[1] = static_cast<uint32_t>(D::narrow(x[2])) | (static_cast<uint32_t>(D::narrow(x[3])) << 16);
+    __builtin_nontemporal_store(w, reinterpret_cast<u2*>(p));
+  } else {
+    stq(static_cast<float*>(p), x);
+  }
+}
+
+// `p` advanced by `elems` elements of `bytes` each is aligned for a quad
+__device__ inline bool quad_aligned(const void* p, int64_t elems, int bytes) {
+  return ((reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(elems * bytes)) &
+          static_cast<uintptr_t>(4 * bytes - 1)) == 0;
 }
 
 template <class D>
@@ -333,16 +378,21 @@ struct GradScan {
     for (int64_t i = b8 + lane; i < b; i += kScanThreads) element(sg, i, count);
     const int64_t ng = (b8 - a8) / kVec;
     const char* src = static_cast<const char*>(sg.grad) + (a8 - sg.begin) * G::kBytes;
+    // kScanDepth groups in flight per lane; each lane still takes its
+    // groups j, j + kScanThreads, ... in increasing order, so its running
+    // sum (and the block's partial) does not depend on the depth
+    constexpr int kWords = kVec * G::kBytes / 4;
     int64_t j = lane;
-    for (; j + kScanThreads < ng; j += 2 * kScanThreads) {   // two groups in flight per lane
-      uint32_t w0[kVec * G::kBytes / 4], w1[kVec * G::kBytes / 4];
-      load_words<G>(src + j * (kVec * G::kBytes), w0);
-      load_words<G>(src + (j + kScanThreads) * (kVec * G::kBytes), w1);
-      group(sg, w0, a8 + j * kVec, count);
-      group(sg, w1, a8 + (j + kScanThreads) * kVec, count);
+    for (; j + (kScanDepth - 1) * kScanThreads < ng; j += kScanDepth * kScanThreads) {
+      uint32_t w[kScanDepth][kWords];
+#pragma unroll
+      for (int d = 0; d < kScanDepth; ++d)
+        load_words<G>(src + (j + d * kScanThreads) * (kVec * G::kBytes), w[d]);
+#pragma unroll
+      for (int d = 0; d < kScanDepth; ++d) group(sg, w[d], a8 + (j + d * kScanThreads) * kVec, count);
     }
-    if (j < ng) {
-      uint32_t w0[kVec * G::kBytes / 4];
+    for (; j < ng; j += kScanThreads) {
+      uint32_t w0[kWords];
       load_words<G>(src + j * (kVec * G::kBytes), w0);
       group(sg, w0, a8 + j * kVec, count);
     }
@@ -532,8 +582,14 @@ __device__ inline void adamw1(float g, float& p, float& m, float& v,
   p = p + (h.neg_lr * (m / h.bc1)) / den;
 }
 
+// One block per kStreamTile-element tile (grid-stride when the grid is
+// clamped).  A tile inside one segment whose grad / model addresses are
+// quad-aligned takes the vector path: each lane streams kStreamUnroll quads
+// in wave order, all loads of the tile first, then the arithmetic and all
+// stores.  Other tiles (segment edges, the tail, misaligned storage) go
+// element by element: lane j takes elements j, j + kStreamThreads, ...
 template <class G, class M, bool kFlatGrad>
-__global__ __launch_bounds__(kThreads) void k_adamw(
+__global__ __launch_bounds__(kStreamThreads) void k_adamw(
     float* __restrict__ master, float* __restrict__ exp_avg,
     float* __restrict__ exp_avg_sq, const float* __restrict__ flat_grad,
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
@@ -543,58 +599,55 @@ __global__ __launch_bounds__(kThreads) void k_adamw(
   const float coef = sc->coef;
   const int lane = threadIdx.x;
   const int64_t n = end - begin;
-  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const int64_t ntiles = (n + kStreamTile - 1) / kStreamTile;
   const bool arrays_vec = aligned16(master) && aligned16(exp_avg) &&
                           aligned16(exp_avg_sq) &&
                           (!kFlatGrad || aligned16(flat_grad));
 
   for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    const int64_t t0 = begin + t * kTile;
-    const int64_t t1 = (t0 + kTile < end) ? t0 + kTile : end;
+    const int64_t t0 = begin + t * kStreamTile;
+    const int64_t t1 = (t0 + kStreamTile < end) ? t0 + kStreamTile : end;
     const int s = find_seg(segs, nseg, t0);
     const ms_segment_t seg = segs[s];
-    const bool fast = t1 - t0 == kTile && t0 >= seg.begin && t1 <= seg_end(seg) && arrays_vec &&
-                      ((t0 - seg.begin) & (kVec - 1)) == 0 &&
-                      (kFlatGrad || aligned16(seg.grad)) && aligned16(seg.model);
-    const int64_t i0 = t0 + static_cast<int64_t>(lane) * kVec;
-    const int64_t li = i0 - begin;
+    const int64_t so = t0 - seg.begin;   // the tile's offset in the segment
+    const bool fast = t1 - t0 == kStreamTile && so >= 0 && t1 <= seg_end(seg) && arrays_vec &&
+                      (kFlatGrad || seg.grad == nullptr || quad_aligned(seg.grad, so, G::kBytes)) &&
+                      (seg.model == nullptr || quad_aligned(seg.model, so, M::kBytes));
     if (fast) {
-      float g[kVec], p[kVec], m[kVec], v[kVec];
-      if (kFlatGrad) {
-        load_f8(flat_grad + li, g);
-      } else if (seg.grad) {
-        typename G::raw r[kVec];
-        load_raw8<G>(static_cast<const char*>(seg.grad) +
-                         (i0 - seg.begin) * G::kBytes,
-                     r);
+      const int64_t tl = t0 - begin;     // the tile's offset in the state arrays
+      float g[kStreamUnroll][4], p[kStreamUnroll][4], m[kStreamUnroll][4], v[kStreamUnroll][4];
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) {
-          g[k] = unscale1(G::widen(r[k]), h.umode, h.grad_scale, h.inv_scale);
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
+        if (kFlatGrad) {
+          ldq(flat_grad + tl + e, g[u]);
+        } else if (seg.grad) {
+          ldq_raw<G>(static_cast<const char*>(seg.grad) + (so + e) * G::kBytes, g[u]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) g[u][k] = 0.0f;
         }
-      } else {
-#pragma unroll
-        for (int k = 0; k < kVec; ++k) g[k] = 0.0f;
+        ldq(master + tl + e, p[u]);
+        ldq(exp_avg + tl + e, m[u]);
+        ldq(exp_avg_sq + tl + e, v[u]);
       }
-      load_f8(master + li, p);
-      load_f8(exp_avg + li, m);
-      load_f8(exp_avg_sq + li, v);
 #pragma unroll
-      for (int k = 0; k < kVec; ++k) adamw1(g[k], p[k], m[k], v[k], h, clip, coef);
-      store_f8(master + li, p);
-      store_f8(exp_avg + li, m);
-      store_f8(exp_avg_sq + li, v);
-      if (seg.model) {
-        typename M::raw o[kVec];
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) o[k] = M::narrow(p[k]);
-        store_raw8<M>(static_cast<char*>(seg.model) +
-                          (i0 - seg.begin) * M::kBytes,
-                      o);
+        for (int k = 0; k < 4; ++k) {
+          if (!kFlatGrad && seg.grad) g[u][k] = unscale1(g[u][k], h.umode, h.grad_scale, h.inv_scale);
+          adamw1(g[u][k], p[u][k], m[u][k], v[u][k], h, clip, coef);
+        }
+        stq(master + tl + e, p[u]);
+        stq(exp_avg + tl + e, m[u]);
+        stq(exp_avg_sq + tl + e, v[u]);
+        if (seg.model) stq_raw<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, p[u]);
       }
     } else {
       int sl = s;
-      for (int k = 0; k < kVec; ++k) {
-        const int64_t i = i0 + k;
+      for (int k = 0; k < 4 * kStreamUnroll; ++k) {
+        const int64_t i = t0 + lane + static_cast<int64_t>(k) * kStreamThreads;
         if (i >= t1) break;
         while (sl + 1 < nseg && i >= seg_end(segs[sl])) ++sl;
         const ms_segment_t& sg = segs[sl];
@@ -619,36 +672,40 @@ __global__ __launch_bounds__(kThreads) void k_adamw(
 }
 
 // ------------------------------------------------------------------ K4
+// The tiling and vector / element paths of K3, with one read and one write
+// stream.
 template <class M>
-__global__ __launch_bounds__(kCastThreads) void k_cast(
+__global__ __launch_bounds__(kStreamThreads) void k_cast(
     const float* __restrict__ flat, const ms_segment_t* __restrict__ segs,
     int nseg, int64_t begin, int64_t end) {
   const int lane = threadIdx.x;
   const int64_t n = end - begin;
-  const int64_t ntiles = (n + kCastTile - 1) / kCastTile;
+  const int64_t ntiles = (n + kStreamTile - 1) / kStreamTile;
   const bool flat_vec = aligned16(flat);
   for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    const int64_t t0 = begin + t * kCastTile;
-    const int64_t t1 = (t0 + kCastTile < end) ? t0 + kCastTile : end;
+    const int64_t t0 = begin + t * kStreamTile;
+    const int64_t t1 = (t0 + kStreamTile < end) ? t0 + kStreamTile : end;
     const int s = find_seg(segs, nseg, t0);
     const ms_segment_t seg = segs[s];
-    const bool fast = t1 - t0 == kCastTile && t0 >= seg.begin && t1 <= seg_end(seg) && flat_vec &&
-                      ((t0 - seg.begin) & (kVec - 1)) == 0 &&
-                      aligned16(seg.model);
-    const int64_t i0 = t0 + static_cast<int64_t>(lane) * kVec;
+    const int64_t so = t0 - seg.begin;
+    const bool fast = t1 - t0 == kStreamTile && so >= 0 && t1 <= seg_end(seg) && flat_vec &&
+                      quad_aligned(seg.model, so, M::kBytes);
     if (fast) {
       if (!seg.model) continue;
-      float x[kVec];
-      load_f8(flat + (i0 - begin), x);
-      typename M::raw o[kVec];
+      const int64_t tl = t0 - begin;
+      float x[kStreamUnroll][4];
 #pragma unroll
-      for (int k = 0; k < kVec; ++k) o[k] = M::narrow(x[k]);
-      store_raw8<M>(static_cast<char*>(seg.model) + (i0 - seg.begin) * M::kBytes,
-                    o);
+      for (int u = 0; u < kStreamUnroll; ++u)
+        ldq(flat + tl + 4 * (static_cast<int64_t>(u) * kStreamThreads + lane), x[u]);
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
+        stq_raw<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, x[u]);
+      }
     } else {
       int sl = s;
-      for (int k = 0; k < kVec; ++k) {
-        const int64_t i = i0 + k;
+      for (int k = 0; k < 4 * kStreamUnroll; ++k) {
+        const int64_t i = t0 + lane + static_cast<int64_t>(k) * kStreamThreads;
         if (i >= t1) break;
         while (sl + 1 < nseg && i >= seg_end(segs[sl])) ++sl;
         const ms_segment_t& sg = segs[sl];
@@ -834,9 +891,9 @@ void launch_adamw(float* p, float* m, float* v, const float* fg,
                   const ms_segment_t* segs, int nseg, int64_t begin, int64_t end,
                   const AdamScalars& h, const ms_step_scalars_t* sc,
                   hipStream_t st) {
-  const int64_t ntiles = (end - begin + kTile - 1) / kTile;
+  const int64_t ntiles = (end - begin + kStreamTile - 1) / kStreamTile;
   const dim3 grid(stream_grid(ntiles));
-  const dim3 block(kThreads);
+  const dim3 block(kStreamThreads);
   if (fg)
     hipLaunchKernelGGL((k_adamw<G, M, true>), grid, block, 0, st, p, m, v, fg,
                        segs, nseg, begin, end, h, sc);
@@ -1038,9 +1095,9 @@ int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
   if (!flat) return MS_EINVAL;
   if (!segs || nseg <= 0 || nseg > kMaxSegs) return MS_ETABLE;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t ntiles = (end - begin + kCastTile - 1) / kCastTile;
+  const int64_t ntiles = (end - begin + kStreamTile - 1) / kStreamTile;
   const dim3 grid(stream_grid(ntiles));
-  const dim3 block(kCastThreads);
+  const dim3 block(kStreamThreads);
   switch (model_dtype) {
     case MS_DTYPE_F32:
       hipLaunchKernelGGL(k_cast<DF32>, grid, block, 0, st, flat, segs, nseg,
