@@ -2,17 +2,21 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload gpt-1.3b | llama3-8b-shard]
                     [--grad-dtype fp16] [--mode fused|materialize|contiguous] [--zero-stage 1]
-                    [--no-cpu-baseline] [--copy-calibration]
+                    [--state-spacing-gib auto] [--no-cpu-baseline] [--copy-calibration]
+                    [--hbm-ceilings]
 
 A step is one gradient-accumulation boundary through the engine API
 (``engine.step()``): the ragged-grad scan, the norm/clip/skip decision and
 the fused AdamW + model cast, plus the one read-back of the step scalars and
-the host bookkeeping.  Each timed step is one ``engine.step()`` call
-bracketed by ``torch.cuda.synchronize()`` on both sides; ``ms_per_step`` is
-their mean.  The gradients are resident in HBM before each timed step: one
-of two pre-generated gradient sets is re-attached to ``param.grad`` (what
-the last ``backward`` of a window leaves) outside the bracket;
-``ms_per_step_with_grad_attach`` is the whole loop including that.
+the host bookkeeping.  Before each step one of two pre-generated gradient
+sets, resident in HBM, is re-attached to ``param.grad`` (what the last
+``backward`` of a window leaves).  The K timed steps run back to back,
+bracketed as a whole by ``torch.cuda.synchronize()``; ``ms_per_step`` is
+the bracket over K.  The same steps are then run one at a time, each
+bracketed on its own (``ms_per_step_synced``: the latency of one boundary,
+host work before the first kernel included).  A second, shorter run with
+the masters and moments in separate allocations is reported next to the
+engine's default placement (``separate_allocations``).
 
 Workload (default): the 1.3B GPT-style buffer (24 layers, d 2048, vocab
 50257, 292 ragged tensors, 1,315,723,264 params), fp16 gradients
@@ -64,6 +68,10 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def _spacing(text: str):
+    return "auto" if text == "auto" else float(text)
+
+
 def parse(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,8 +82,11 @@ def parse(argv=None):
     ap.add_argument("--mode", default="fused", choices=["fused", "materialize", "contiguous"])
     ap.add_argument("--zero-stage", type=int, default=1, choices=[0, 1, 2, 3],
                     help="ZeRO stage at world size 1 (3: also times the parameter gather)")
-    ap.add_argument("--state-spacing-gib", type=float, default=32.0,
-                    help="hip_boundary.state_spacing_gib of the engine (0: masters and moments packed)")
+    ap.add_argument("--state-spacing-gib", type=_spacing, default="auto",
+                    help="hip_boundary.state_spacing_gib of the engine: auto (the engine's default), "
+                         "0 (separate allocations) or a window in GiB")
+    ap.add_argument("--no-compare-separate", dest="compare_separate", action="store_false",
+                    help="skip the second, shorter run with the state in separate allocations")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without the per-kernel HIP events (no roofline)")
@@ -88,7 +99,7 @@ def parse(argv=None):
     return ap.parse_args(argv)
 
 
-def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1, state_spacing_gib: float = 32.0) -> dict:
+def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1, state_spacing_gib="auto") -> dict:
     cfg = {
         "train_micro_batch_size_per_gpu": 1,
         "gradient_accumulation_steps": 1,
@@ -199,7 +210,7 @@ def bench_llama_shard(args) -> dict:
 
     from minispeed_amd import _native
     from minispeed_amd.boundary import LaunchTimer, adamw_params
-    from minispeed_amd.flat import STATE_SPACING_BYTES, FlatLayout, check_table, state_buffers
+    from minispeed_amd.flat import AUTO_SPACING, FlatLayout, check_table, state_buffers
     from minispeed_amd.workloads import shapes_of
 
     lib = _native.load()
@@ -213,8 +224,8 @@ def bench_llama_shard(args) -> dict:
     log(f"[bench] llama3-8b: {len(shapes)} tensors, {N:,} params; rank 3 of 8 owns [{lo:,}, {hi:,})")
     gen = torch.Generator(device=dev).manual_seed(5)
     # the partitioned masters and the moments, placed as the engine places
-    # them with hip_boundary.state_spacing_gib = 32
-    master, m, v = state_buffers([[S, S, S]], dev, STATE_SPACING_BYTES)[0]
+    # them by default
+    master, m, v = state_buffers([[S, S, S]], dev, AUTO_SPACING)[0]
     master.normal_(0.0, 0.02, generator=gen)
     grad = torch.empty(S, dtype=torch.bfloat16, device=dev)
     for a in range(0, S, 1 << 27):   # bounded fp32 temporaries
@@ -238,9 +249,12 @@ def bench_llama_shard(args) -> dict:
     pflag = torch.empty(nb, dtype=torch.int32, device=dev)
     scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=dev)
     host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
+    k2_done = torch.cuda.Event()
     timer = LaunchTimer()
 
     def step(k: int, timed: bool) -> None:
+        """K1 -> K2 -> K3 with the engine's one host wait: for K2's scalars,
+        written straight to pinned host memory, while K3 runs on."""
         t = timer if timed else None
         hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, k + 1)
         tok = t.start("k1") if t else None
@@ -250,8 +264,9 @@ def bench_llama_shard(args) -> dict:
         if t:
             t.stop(tok)
         _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 1.0, 0, 1.0,
-                                       0, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), None, stream),
-                      "ms_norm_clip")
+                                       0, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), host.data_ptr(),
+                                       stream), "ms_norm_clip")
+        k2_done.record()
         tok = t.start("k3") if t else None
         _native.check(lib.ms_fused_adamw(master.data_ptr(), m.data_ptr(), v.data_ptr(), None,
                                          tdev.data_ptr(), len(table), _native.DTYPE_BF16,
@@ -259,17 +274,16 @@ def bench_llama_shard(args) -> dict:
                                          scal.data_ptr(), stream), "ms_fused_adamw")
         if t:
             t.stop(tok)
-        host.copy_(scal, non_blocking=True)
-        torch.cuda.current_stream(dev).synchronize()
+        k2_done.synchronize()
 
     for k in range(args.warmup):
         step(k, False)
-    step_s = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     for k in range(args.steps):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
         step(args.warmup + k, True)
-        step_s.append(time.perf_counter() - t0)
+    torch.cuda.synchronize()
+    step_s = [(time.perf_counter() - t0) / args.steps]
     res = _native.StepScalars.from_buffer_copy(host.numpy().tobytes())
     # norm = sqrt(S * 1e-8) ~ 3.2 > clip 1.0: the clip path is exercised
     if res.overflow or not res.clip_applied:
@@ -332,11 +346,16 @@ def traffic_for(kernel: str, workload: str, grad_dtype: str, mode: str, spacing_
 
 
 def bench_hbm_ceilings(args) -> dict:
-    """Streaming-bandwidth reference points on 4 GiB fp32 buffers (1 GiB for
-    the half-precision streams): what one read-only stream, one write-only
-    stream, a 1:1 copy and a 2:1 add reach on this GPU, next to K3 itself
-    over contiguous arrays with the masters and moments in a 32 GiB-window
-    arena and in separate allocations.  Median of 10 launches after 3, HIP
+    """What this GPU's HBM sustains for each mix of streams the boundary
+    kernels use, measured with the streaming probes of libms_hbm_probe.so,
+    independent of the boundary kernels: one read stream, one write stream,
+    a copy, in-place read-modify-write of one and of three arrays (AdamW's
+    p, m, v) and K3's whole mix (three read-modify-write arrays plus one read
+    and one write array), 4 GiB per array, the arrays 32 GiB apart (the
+    placement of the state arena).  Each mix is run over a grid of launch
+    shapes (threads per block, 16-byte vectors per lane, lane or wave order,
+    non-temporal hints) and the fastest is reported; then K3 itself over
+    2^30 elements in the same placement.  Median of 6 launches after 2, HIP
     events on the current stream; bytes are the algorithmic ones."""
     import ctypes
 
@@ -345,19 +364,32 @@ def bench_hbm_ceilings(args) -> dict:
 
     from minispeed_amd import _native
     from minispeed_amd.boundary import adamw_params
-    from minispeed_amd.flat import STATE_SPACING_BYTES, FlatLayout, state_buffers
 
-    lib = _native.load()
     dev = torch.device("cuda", 0)
     stream = _native.stream_handle(dev)
-    n = 1 << 30
+    probe = ctypes.CDLL(os.path.join(ROOT, "minispeed_amd", "libms_hbm_probe.so"))
+    P = ctypes.c_void_p
+    probe.msp_stream.restype = ctypes.c_int
+    probe.msp_stream.argtypes = [ctypes.POINTER(P), ctypes.c_int32, ctypes.POINTER(P), ctypes.c_int32,
+                                 ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                 ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, P, P]
+    gib = 1 << 30
+    nbytes = 4 * gib
+    arena = torch.empty(4 * 32 * gib + nbytes, dtype=torch.uint8, device=dev)
+    base = arena.data_ptr()
+    at = [base + k * 32 * gib for k in range(5)]
+    for a in at:
+        assert a + nbytes <= base + arena.numel()
+    for k in range(5):
+        arena[k * 32 * gib:k * 32 * gib + nbytes].fill_(1)
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
 
-    def median_ms(fn):
-        for _ in range(3):
+    def median_ms(fn, reps=6, warm=2):
+        for _ in range(warm):
             fn()
         torch.cuda.synchronize()
         evs = []
-        for _ in range(10):
+        for _ in range(reps):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             fn()
@@ -366,52 +398,55 @@ def bench_hbm_ceilings(args) -> dict:
         torch.cuda.synchronize()
         return float(np.median([a.elapsed_time(b) for a, b in evs]))
 
+    mixes = {
+        "read": ([at[0]], []), "write": ([], [at[0]]), "copy": ([at[0]], [at[1]]),
+        "rmw_1_array": ([at[0]], [at[0]]),
+        "rmw_3_arrays": (at[:3], at[:3]),
+        "k3_mix": (at[:4], at[:3] + [at[4]]),
+    }
     out = {}
+    for name, (rd, wr) in mixes.items():
+        rdp = (P * 4)(*rd, *([0] * (4 - len(rd))))
+        wrp = (P * 4)(*wr, *([0] * (4 - len(wr))))
+        best = None
+        for threads in (128, 256):
+            for unroll in (1, 2, 4):
+                for wave in (0, 1):
+                    for ntl, nts in ((1, 1), (1, 0), (0, 1), (0, 0)):
+                        if (not rd and ntl) or (not wr and nts):
+                            continue
 
-    def record(name, nbytes, ms):
-        out[name] = {"ms": round(ms, 4), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-        log(f"[bench] {name}: {ms:.3f} ms, {out[name]['gbps']:.0f} GB/s")
+                        def fn():
+                            rc = probe.msp_stream(rdp, len(rd), wrp, len(wr), nbytes // 16, threads, unroll,
+                                                  wave, 0, ntl, nts, sink.data_ptr(), stream)
+                            if rc != 0:
+                                raise RuntimeError(f"msp_stream failed with {rc}")
+                        ms = median_ms(fn)
+                        if best is None or ms < best["ms"]:
+                            best = {"ms": round(ms, 4), "threads": threads, "unroll": unroll,
+                                    "order": "wave" if wave else "lane", "nt_load": ntl, "nt_store": nts}
+        best["gbps"] = round(nbytes * (len(rd) + len(wr)) / (best["ms"] * 1e-3) / 1e9, 1)
+        out[name] = best
+        log(f"[bench] {name}: {best['gbps']:.0f} GB/s ({best})")
 
-    x = torch.ones(n, device=dev)
-    nb = _native.stats_blocks()
-    psum = torch.empty(nb, dtype=torch.float64, device=dev)
-    pflag = torch.empty(nb, dtype=torch.int32, device=dev)
-    table = torch.from_numpy(np.array([[0, n, x.data_ptr(), 0]], dtype=np.int64)).to(dev)
-
-    def read_only():
-        _native.check(lib.ms_grad_stats(table.data_ptr(), 1, _native.DTYPE_F32, 0, n, 0, n,
-                                        _native.SCALE_NONE, 1.0, None, psum.data_ptr(),
-                                        pflag.data_ptr(), nb, stream), "ms_grad_stats")
-    record("read_only_k1_fp32", 4 * n, median_ms(read_only))
-    record("write_only_fill", 4 * n, median_ms(lambda: x.fill_(1.0)))
-    y = torch.empty_like(x)
-    record("copy_1_to_1", 8 * n, median_ms(lambda: y.copy_(x)))
-    z = torch.empty_like(x)
-    record("add_2_to_1", 12 * n, median_ms(lambda: torch.add(x, y, out=z)))
-    del x, y, z, table
-    torch.cuda.empty_cache()
-
+    lib = _native.load()
+    n = 1 << 30
     g = torch.full((n,), 0.5, dtype=torch.float16, device=dev)
     model = torch.empty(n, dtype=torch.float16, device=dev)
-    lay = FlatLayout([n], rank=0, world_size=1, zero_stage=1)
-    tab = torch.from_numpy(lay.segments(0, n, [(g.data_ptr(), (0, n), 2)],
-                                        [(model.data_ptr(), (0, n), 2)])).to(dev)
+    tab = torch.tensor([[0, n, g.data_ptr(), model.data_ptr()]], dtype=torch.int64, device=dev)
     hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 10)
     clean = torch.zeros(_native.SCALARS_BYTES, dtype=torch.uint8, device=dev)
-    for name, window in (("k3_arena_32gib", STATE_SPACING_BYTES), ("k3_separate", 0)):
-        p, m, v = state_buffers([[n, n, n]], dev, window)[0]
-        p.fill_(0.01)
 
-        def k3():
-            _native.check(lib.ms_fused_adamw(p.data_ptr(), m.data_ptr(), v.data_ptr(), None,
-                                             tab.data_ptr(), tab.shape[0], _native.DTYPE_F16,
-                                             _native.DTYPE_F16, 0, n, ctypes.byref(hp),
-                                             clean.data_ptr(), stream), "ms_fused_adamw")
-        record(name, 28 * n, median_ms(k3))
-        del p, m, v
-        torch.cuda.empty_cache()
-    return {"hbm_ceilings": out, "elements": n, "peak_gbps": 8000.0,
-            "note": "fp32 buffers of 4 GiB; K3 moves 28 B per element (fp16 grads and model copy)"}
+    def k3():
+        _native.check(lib.ms_fused_adamw(at[0], at[1], at[2], None, tab.data_ptr(), 1, _native.DTYPE_F16,
+                                         _native.DTYPE_F16, 0, n, ctypes.byref(hp), clean.data_ptr(),
+                                         stream), "ms_fused_adamw")
+    ms = median_ms(k3)
+    out["k3_adamw"] = {"ms": round(ms, 4), "gbps": round(28 * n / (ms * 1e-3) / 1e9, 1),
+                       "note": "2^30 elements, fp16 grads and model copy in separate allocations"}
+    log(f"[bench] K3: {out['k3_adamw']['gbps']:.0f} GB/s")
+    return {"hbm_ceilings": out, "bytes_per_array": nbytes, "peak_gbps": PEAK_GBPS,
+            "placement": "arrays 32 GiB apart in one allocation"}
 
 
 def main(argv=None) -> int:
@@ -446,84 +481,112 @@ def main(argv=None) -> int:
     gdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.grad_dtype]
     log(f"[bench] workload {args.workload}: {len(shapes)} tensors, {n_params:,} params, "
         f"grads {args.grad_dtype}, mode {args.mode}")
-
     gen = torch.Generator(device=dev).manual_seed(1234)
-    params = [nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
-    module = nn.ParameterList(params)
-    engine = ms.initialize(model=module, model_parameters=list(module),
-                           config=engine_config(args.grad_dtype, args.mode, args.zero_stage,
-                                                args.state_spacing_gib))
     mult = 2.0 ** 16 if args.grad_dtype == "fp16" else 1.0
     grad_sets = []
-    for _ in range(2):
-        grad_sets.append([(torch.randn(*s, generator=gen, device=dev) * (1e-3 * mult)).to(gdt)
-                          for s in shapes])
-    torch.cuda.synchronize()
-    log("[bench] buffers resident; warming up")
 
-    gather_s = []
-    accum_s = []
+    def run_engine(spacing, steps: int, kernel_timing: bool) -> dict:
+        """Build an engine with this state placement, warm it up and time
+        ``steps`` boundaries back to back and then one at a time.  As in
+        training, the engine (and its state) is built before the gradients
+        exist; two gradient sets are made once and shared by every run."""
+        params = [nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
+        module = nn.ParameterList(params)
+        engine = ms.initialize(model=module, model_parameters=list(module),
+                               config=engine_config(args.grad_dtype, args.mode, args.zero_stage, spacing))
+        while len(grad_sets) < 2:
+            grad_sets.append([(torch.randn(*s, generator=gen, device=dev) * (1e-3 * mult)).to(gdt)
+                              for s in shapes])
+        g0 = engine.flat_groups[0]
+        st0 = engine.optimizer.state[0]
+        same = st0["exp_avg"].untyped_storage().data_ptr() == g0.data.untyped_storage().data_ptr()
+        window = (st0["exp_avg"].data_ptr() - g0.data.data_ptr()) / 2 ** 30 if same else 0.0
+        torch.cuda.synchronize()
+        log(f"[bench] state placement {spacing!r}: window {window:g} GiB; warming up")
+        gather_s, accum_s = [], []
 
-    def attach(k: int) -> None:
-        """What the last backward of a window leaves: grads on every param
-        (ZeRO-3: after the forward's parameter gather, timed on its own)."""
-        if args.zero_stage == 3:
+        def attach(k: int) -> None:
+            """What the last backward of a window leaves: grads on every param
+            (ZeRO-3: after the forward's parameter gather, timed on its own)."""
+            if args.zero_stage == 3:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                engine.optimizer.gather_parameters()
+                torch.cuda.synchronize()
+                gather_s.append(time.perf_counter() - t0)
+            for p, g in zip(params, grad_sets[k % 2]):
+                p.grad = g
+            if engine.contiguous is not None:
+                # what the post-accumulate-grad hooks do during the backward of a
+                # one-micro-batch window, timed on its own
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for i, p in enumerate(params):
+                    engine.contiguous.accumulate(0, i, p)
+                torch.cuda.synchronize()
+                accum_s.append(time.perf_counter() - t0)
+            engine.micro_steps += 1
+
+        def boundary() -> None:
+            if not engine.step():
+                raise RuntimeError("boundary step was skipped (unexpected overflow)")
+
+        for k in range(args.warmup):
+            attach(k)
+            boundary()
+        torch.cuda.synchronize()
+        gather_s.clear()
+        accum_s.clear()
+        # 2 events per kernel launch (K1 and K3 per group, K2 once), created
+        # before the timed loop
+        timer = LaunchTimer(reserve=2 * (2 * len(engine.flat_groups) + 1) * steps)
+        engine.optimizer.launch_timer = timer if kernel_timing else None
+        # the timed steps, bracketed as a whole: each step re-attaches its
+        # gradients (what the window's last backward leaves) and runs the
+        # boundary; the host work of step k+1 overlaps K3 of step k
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            attach(k)
+            boundary()                       # ends with the one scalar read-back
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        engine.optimizer.launch_timer = None
+        # the same steps one at a time, each bracketed by synchronisations: the
+        # latency of one boundary, host work before K1 included
+        step_s = []
+        for k in range(steps):
+            attach(k)
             torch.cuda.synchronize()
-            t0 = time.perf_counter()
+            t1 = time.perf_counter()
+            boundary()
+            torch.cuda.synchronize()
+            step_s.append(time.perf_counter() - t1)
+        log(f"[bench] {steps} boundary steps: {elapsed * 1e3:.3f} ms back to back, "
+            f"{sum(step_s) * 1e3:.3f} ms one at a time")
+        out = {"ms_step": elapsed / steps * 1e3, "step_s": step_s, "window_gib": window,
+               "k_ms": ({k: float(np.mean(timer.durations_ms(k))) for k in ("k1", "k2", "k3")}
+                        if kernel_timing else None)}
+        if accum_s:
+            out["accumulate_ms"] = float(np.mean(accum_s)) * 1e3
+        if args.zero_stage == 3:
+            # the gather is a change of views; a stale copy would cost one cast
             engine.optimizer.gather_parameters()
             torch.cuda.synchronize()
-            gather_s.append(time.perf_counter() - t0)
-        for p, g in zip(params, grad_sets[k % 2]):
-            p.grad = g
-        if engine.contiguous is not None:
-            # what the post-accumulate-grad hooks do during the backward of a
-            # one-micro-batch window, timed on its own
-            torch.cuda.synchronize()
             t0 = time.perf_counter()
-            for i, p in enumerate(params):
-                engine.contiguous.accumulate(0, i, p)
+            for g in engine.flat_groups:
+                g.copy_flat_to_model()
             torch.cuda.synchronize()
-            accum_s.append(time.perf_counter() - t0)
-        engine.micro_steps += 1
-
-    def boundary() -> None:
-        if not engine.step():
-            raise RuntimeError("boundary step was skipped (unexpected overflow)")
-
-    for k in range(args.warmup):
-        attach(k)
-        boundary()
-    torch.cuda.synchronize()
-    gather_s.clear()
-    accum_s.clear()
-    # 2 events per kernel launch (K1 and K3 per group, K2 once), created
-    # before the timed loop
-    timer = LaunchTimer(reserve=2 * (2 * len(engine.flat_groups) + 1) * args.steps)
-    engine.optimizer.launch_timer = timer if not args.no_kernel_timing else None
-    # the K timed steps, bracketed as a whole: each step re-attaches its
-    # gradients (what the window's last backward leaves) and runs the
-    # boundary; the host work of step k+1 overlaps K3 of step k
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        attach(k)
-        boundary()                       # ends with the one scalar read-back
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    engine.optimizer.launch_timer = None
-    # the same steps one at a time, each bracketed by synchronisations: the
-    # latency of one boundary, host work before K1 included
-    step_s = []
-    for k in range(args.steps):
-        attach(k)
+            out["zero3"] = {"gather_ms": round(float(np.mean(gather_s)) * 1e3, 4),
+                            "recast_ms": round((time.perf_counter() - t0) * 1e3, 4)}
+        for p in params:
+            p.grad = None
+        del engine, module, params
         torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        boundary()
-        torch.cuda.synchronize()
-        step_s.append(time.perf_counter() - t1)
-    log(f"[bench] {args.steps} boundary steps: {elapsed * 1e3:.3f} ms back to back, "
-        f"{sum(step_s) * 1e3:.3f} ms one at a time")
+        torch.cuda.empty_cache()
+        return out
 
+    head = run_engine(args.state_spacing_gib, args.steps, not args.no_kernel_timing)
     if args.copy_calibration:
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev)   # 1 GiB
         dst = torch.empty_like(src)
@@ -531,18 +594,20 @@ def main(argv=None) -> int:
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
+        del src, dst
         log("[bench] copy calibration: 3 x 1 GiB device copies (read 1 GiB + write 1 GiB each)")
+    # the same workload with the masters and moments in three separate
+    # allocations, for comparison with the placement above
+    other = None
+    if args.compare_separate and head["window_gib"] > 0:
+        other = run_engine(0, max(5, args.steps // 2), not args.no_kernel_timing)
 
-    ms_step = elapsed / args.steps * 1e3
+    ms_step = head["ms_step"]
     esize = 4 if args.grad_dtype == "fp32" else 2
     b1, b3 = BYTES[(args.mode, esize)]
-    if args.no_kernel_timing:
-        k_ms = {k: float("nan") for k in ("k1", "k2", "k3")}
-    else:
-        k_ms = {k: float(np.mean(timer.durations_ms(k))) for k in ("k1", "k2", "k3")}
-    k3_gbps = b3 * n_params / (k_ms["k3"] * 1e-3) / 1e9
+    k_ms = head["k_ms"]
     step_gbps = (b1 + b3) * n_params / (ms_step * 1e-3) / 1e9
-    traffic = traffic_for("k3", args.workload, args.grad_dtype, args.mode, args.state_spacing_gib)
+    traffic = traffic_for("k3", args.workload, args.grad_dtype, args.mode, head["window_gib"])
     result = {
         "metric": METRIC,
         "value": round(n_params / (ms_step * 1e-3) / 1e9, 3),
@@ -551,8 +616,8 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
-        "ms_per_step_synced": round(float(np.mean(step_s)) * 1e3, 4),
-        "ms_per_step_synced_median": round(float(np.median(step_s)) * 1e3, 4),
+        "ms_per_step_synced": round(float(np.mean(head["step_s"])) * 1e3, 4),
+        "ms_per_step_synced_median": round(float(np.median(head["step_s"])) * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -569,13 +634,19 @@ def main(argv=None) -> int:
             "world_size": 1,
             "mode": args.mode,
             "state_spacing_gib": args.state_spacing_gib,
+            "state_window_gib": head["window_gib"],
             "clip": 1.0,
             "bytes_per_param": b1 + b3,
         },
         "hbm_gbps": round(step_gbps, 1),
         "hbm_frac": round(step_gbps / PEAK_GBPS, 4),
-        "kernel_ms": {k: round(v, 4) for k, v in k_ms.items()},
-        "roofline": {
+        "kernel_ms": {k: round(v, 4) for k, v in k_ms.items()} if k_ms else None,
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    if k_ms:
+        k3_gbps = b3 * n_params / (k_ms["k3"] * 1e-3) / 1e9
+        result["roofline"] = {
             "kernel": "K3 k_adamw (fused AdamW + model cast)",
             "bound": "hbm",
             "achieved": round(k3_gbps, 1),
@@ -584,26 +655,20 @@ def main(argv=None) -> int:
             "frac": round(k3_gbps / PEAK_GBPS, 4),
             "traffic": traffic,
             "bytes_per_param": b3,
-        },
-        "cpu_baseline": None,
-    }
-    if args.no_kernel_timing:
-        result["kernel_ms"] = None
-        result["roofline"] = None
-    if accum_s:
-        result["contiguous"] = {"accumulate_ms_per_micro_batch": round(float(np.mean(accum_s)) * 1e3, 4)}
-    if args.zero_stage == 3:
-        # the gather is a change of views; a stale copy would cost one cast
-        engine.optimizer.gather_parameters()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for g in engine.flat_groups:
-            g.copy_flat_to_model()
-        torch.cuda.synchronize()
-        result["zero3"] = {"gather_ms": round(float(np.mean(gather_s)) * 1e3, 4),
-                           "recast_ms": round((time.perf_counter() - t0) * 1e3, 4)}
+        }
+    if other is not None:
+        result["separate_allocations"] = {
+            "ms_per_step": round(other["ms_step"], 4),
+            "value": round(n_params / (other["ms_step"] * 1e-3) / 1e9, 3),
+            "hbm_frac": round((b1 + b3) * n_params / (other["ms_step"] * 1e-3) / 1e9 / PEAK_GBPS, 4),
+            "kernel_ms": ({k: round(v, 4) for k, v in other["k_ms"].items()} if other["k_ms"] else None),
+        }
+    if "accumulate_ms" in head:
+        result["contiguous"] = {"accumulate_ms_per_micro_batch": round(head["accumulate_ms"], 4)}
+    if "zero3" in head:
+        result["zero3"] = head["zero3"]
     if not args.no_cpu_baseline:
-        del grad_sets, engine, params, module
+        del grad_sets
         torch.cuda.empty_cache()
         log("[bench] CPU baseline (oracle restatement on host cores)")
         result["cpu_baseline"] = cpu_baseline(shapes, args.grad_dtype, args.cpu_sample_params)

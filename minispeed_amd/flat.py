@@ -257,9 +257,14 @@ def _flat_view(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
-# Window of the state arena that ``hip_boundary.state_spacing_gib`` asks for
-# when it is turned on (32 GiB).
-STATE_SPACING_BYTES = 32 << 30
+# State placement (``hip_boundary.state_spacing_gib``): AUTO_SPACING picks
+# the window from the state's size (``auto_window``), 0 means separate
+# allocations, a positive value is the window in bytes.
+AUTO_SPACING = -1
+STATE_SPACING_BYTES = 32 << 30       # the window the 8B-param states need
+_AUTO_WINDOW = 32 << 30
+_AUTO_MIN_COLUMN = 1 << 30
+_AUTO_MAX_SHARE = 0.5      # of the free device memory
 _ARENA_SLACK_BYTES = 1 << 30
 _ARENA_ALIGN = 1 << 21
 
@@ -277,36 +282,55 @@ def state_sizes(layout: "FlatLayout", zero_stage: int) -> Tuple[int, int, int]:
     return layout.numel_padded, n_own, n_own
 
 
+def _column_bytes(sizes: Sequence[Sequence[int]]) -> List[int]:
+    """Bytes of each state column (array j of every group, 2 MiB slots)."""
+    k = len(sizes[0])
+    if any(len(row) != k for row in sizes):
+        raise ValueError("every group needs the same number of state arrays")
+    return [sum(_round_up(4 * int(row[j]), _ARENA_ALIGN) for row in sizes) for j in range(k)]
+
+
+def auto_window(sizes: Sequence[Sequence[int]], free_bytes: Optional[int] = None) -> int:
+    """The window ``state_buffers`` uses by default: 32 GiB when the largest
+    column holds between 1 and 32 GiB and the arena (three windows) takes at
+    most half of ``free_bytes`` (when given), else 0, separate allocations
+    (columns under 1 GiB are too small for placement to show; larger states
+    lie far apart anyway)."""
+    if not sizes:
+        return 0
+    cols = _column_bytes(sizes)
+    if not _AUTO_MIN_COLUMN <= max(cols) <= _AUTO_WINDOW:
+        return 0
+    if free_bytes is not None and len(cols) * _AUTO_WINDOW > _AUTO_MAX_SHARE * free_bytes:
+        return 0
+    return _AUTO_WINDOW
+
+
 def state_buffers(sizes: Sequence[Sequence[int]], device: torch.device,
                   window: int) -> List[List[torch.Tensor]]:
     """Zeroed fp32 buffers, ``sizes[g][j]`` elements for array j of group g.
 
-    With ``window`` 0 they are separate allocations.  With a window they are
-    views of one allocation (the state arena) of ``k`` windows of ``window``
-    bytes: array j of every group lies in window j, the groups back to back
-    at the same offsets in every window.  The fused AdamW kernel reads and
-    writes the masters, exp_avg and exp_avg_sq at the same flat index in
-    lockstep, and on MI355X that streams faster when the three are at least
-    ~32 GiB apart in *physical* HBM: 1.3B params, 5.87-5.93 ms with the
-    three 32 GiB apart against 6.0-6.7 ms in separate allocations (whose
-    physical placement varies from process to process) and 6.8 ms packed
-    back to back.  Mapping the same physical chunks at packed or spaced
-    virtual addresses (and the reverse) shows that only the physical
-    distance counts.  A whole window per array is what keeps the distance
-    in every allocator state: the driver builds an allocation from
-    naturally aligned power-of-two physical blocks, so arrays at multiples
-    of 32 GiB in an allocation of whole 32 GiB windows stay 32 GiB (or a
-    multiple) apart, while a tighter arena puts the last array in a smaller
-    block anywhere in memory.  The arena therefore holds ``k * window``
-    bytes (96 GiB at 32 GiB: about 80 GiB more than the state of a
-    1.3B-param group, about 6 GiB more at 8B).  Columns larger than a window
-    are allocated separately (arrays that large lie far apart anyway), and
-    so is everything when the device lacks the free memory (with a log
-    line).  The placement changes no result.
+    With ``window`` 0 they are separate allocations; ``AUTO_SPACING`` picks
+    the window with :func:`auto_window`.  With a window they are views of
+    one allocation, the state arena (:func:`arena_layout`): array j of every
+    group starts at ``j * window``, the groups back to back at the same
+    offsets in every window.  The fused AdamW kernel reads and writes the
+    masters, exp_avg and exp_avg_sq at the same flat index in lockstep, and
+    on MI355X that streams fastest when the three lie far apart in
+    *physical* HBM, which the runtime decides when it backs an allocation
+    with memory.  Measured on the 1.3B-param state (three 4.9 GiB arrays),
+    K3's time in fresh bench processes: separate allocations 6.5-6.9 ms,
+    one packed allocation 6.7-6.8 ms, three 32 GiB windows 5.73-6.06 ms
+    (every box tried), 16 GiB windows 5.71-5.73 ms on some boxes and
+    6.43-6.55 ms on others.  Columns larger than the window are allocated
+    separately, and so is everything when the device lacks the free memory
+    (with a log line).  The placement changes no result.
     """
     def plain() -> List[List[torch.Tensor]]:
         return [[torch.zeros(int(n), dtype=torch.float32, device=device) for n in row] for row in sizes]
 
+    if window == AUTO_SPACING:
+        window = auto_window(sizes, torch.cuda.mem_get_info(device)[0])
     layout = arena_layout(sizes, window)
     if layout is None:
         return plain()
@@ -325,23 +349,22 @@ def arena_layout(sizes: Sequence[Sequence[int]],
                  window: int) -> Optional[Tuple[List[List[int]], int]]:
     """Byte offsets of ``state_buffers``' arena: ``(starts, total)`` with
     ``starts[g][j]`` the start of array j of group g (fp32 elements
-    ``sizes[g][j]``) and ``total`` the arena size, or None for separate
-    allocations (no window, nothing to place, or a column that does not fit
-    in one window).  Windows and slots are rounded up to 2 MiB."""
+    ``sizes[g][j]``) and ``total`` the arena size, ``k`` whole windows.  None
+    for separate allocations (no window, nothing to place, or a column that
+    does not fit in one window).  Windows and slots are rounded up to 2 MiB."""
     if window <= 0 or not sizes:
         return None
-    k = len(sizes[0])
-    if any(len(row) != k for row in sizes):
-        raise ValueError("every group needs the same number of state arrays")
+    cols = _column_bytes(sizes)
+    k = len(cols)
     window = _round_up(int(window), _ARENA_ALIGN)
+    if max(cols) > window:
+        return None
     fill = [0] * k
     starts = []
     for row in sizes:
         starts.append([j * window + fill[j] for j in range(k)])
         for j, n in enumerate(row):
             fill[j] += _round_up(4 * int(n), _ARENA_ALIGN)
-    if max(fill) > window:
-        return None
     return starts, k * window
 
 

@@ -474,7 +474,7 @@ def test_zero_size_parameter_in_the_list(stage):
 
 def test_state_arena_windows():
     """With a window the buffers are zeroed views of one allocation of three
-    windows: array j of every group in window j, the groups back to back at
+    windows: array j of every group at window j, the groups back to back at
     the same offsets (2 MiB aligned); a column larger than a window, or no
     window, gives separate allocations."""
     from minispeed_amd.flat import state_buffers

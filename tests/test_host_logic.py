@@ -79,10 +79,12 @@ def test_defaults_and_clip_and_scaler_keys():
         DeepSpeedConfig({"scheduler": {"type": "OneCycle"}})
     assert DeepSpeedConfig({"hip_boundary": {"materialize_flat_grad": True}}).materialize_flat_grad
     assert not DeepSpeedConfig({}).materialize_flat_grad
-    assert DeepSpeedConfig({}).state_spacing_bytes == 0
+    assert DeepSpeedConfig({}).state_spacing_bytes == -1            # auto
+    assert DeepSpeedConfig({"hip_boundary": {"state_spacing_gib": "auto"}}).state_spacing_bytes == -1
+    assert DeepSpeedConfig({"hip_boundary": {"state_spacing_gib": 0}}).state_spacing_bytes == 0
     assert DeepSpeedConfig({"hip_boundary": {"state_spacing_gib": 32}}).state_spacing_bytes == 32 << 30
     assert DeepSpeedConfig({"hip_boundary": {"state_spacing_gib": 1.5}}).state_spacing_bytes == 3 << 29
-    for bad in (-1, "32", True, None):
+    for bad in (-1, "32", "Auto", True, None):
         with pytest.raises(ConfigError):
             DeepSpeedConfig({"hip_boundary": {"state_spacing_gib": bad}})
 

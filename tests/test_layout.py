@@ -142,13 +142,14 @@ def test_gpt_workload_shapes_match_reference_counts():
 
 
 def test_state_arena_layout():
-    """Array j of every group in window j, groups back to back at equal
-    offsets, 2 MiB slots; None when a column overflows its window."""
+    """Array j of every group at window j, groups back to back at equal
+    offsets, 2 MiB slots, k whole windows; None when a column overflows its
+    window."""
     from minispeed_amd.flat import arena_layout
 
     mib = 1 << 20
     starts, total = arena_layout([[1000, 700, 700], [mib // 4 + 3, mib // 4 + 3, 5]], 8 * mib)
-    assert total == 24 * mib
+    assert total == 3 * 8 * mib
     assert starts == [[0, 8 * mib, 16 * mib], [2 * mib, 10 * mib, 18 * mib]]
     # an 11 MiB window is rounded up to 12 MiB
     assert arena_layout([[1, 1, 1]], 11 * mib) == ([[0, 12 * mib, 24 * mib]], 36 * mib)
@@ -164,3 +165,20 @@ def test_state_arena_layout():
     n = 1_315_723_264
     starts, total = arena_layout([[n, n, n]], 32 << 30)
     assert starts == [[0, 32 << 30, 64 << 30]] and total == 96 << 30
+
+
+def test_auto_window_is_32_gib_for_states_of_1_to_32_gib_per_array():
+    from minispeed_amd.flat import auto_window
+
+    gib = 1 << 30
+    n13 = 1_315_723_264                                       # 1.3B GPT: 4.9 GiB arrays
+    assert auto_window([[n13, n13, n13]]) == 32 * gib
+    n8 = 8_030_261_248                                        # Llama-3-8B whole: 29.9 GiB
+    assert auto_window([[n8, n8, n8]]) == 32 * gib
+    assert auto_window([[3_323_392] * 3]) == 0                # tiny LM: 13 MB arrays
+    assert auto_window([[n8 + n13] * 3]) == 0                 # 35 GiB: separate
+    assert auto_window([[n13, n13, n13], [n13, n13, n13]]) == 32 * gib     # 9.8 GiB columns
+    assert auto_window([]) == 0
+    # the 96 GiB arena only when it takes at most half of the free memory
+    assert auto_window([[n13, n13, n13]], free_bytes=192 * gib) == 32 * gib
+    assert auto_window([[n13, n13, n13]], free_bytes=191 * gib) == 0
