@@ -217,3 +217,40 @@ def require_hip_tensor(t: torch.Tensor, what: str) -> None:
 
 def stream_handle(device: torch.device) -> int:
     return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+# Timing-only HIP events.  hipEventDisableSystemFence (hip_runtime_api.h)
+# records an event without the system-scope release that a default event
+# performs, i.e. without writing back and invalidating the caches between
+# the kernels it brackets; the elapsed time between two such events is valid
+# once the stream has been synchronised.
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+_hip: Optional[ctypes.CDLL] = None
+
+
+def hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime torch has already loaded (RTLD_NOLOAD: never a second
+    copy), typed for the event calls."""
+    global _hip
+    if _hip is not None:
+        return _hip
+    with _lock:
+        if _hip is None:
+            try:
+                hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD)
+            except OSError as exc:
+                raise NativeLibraryError(f"the HIP runtime is not loaded: {exc}") from exc
+            hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(_P), ctypes.c_uint]
+            hip.hipEventRecord.argtypes = [_P, _P]
+            hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(_F), _P, _P]
+            hip.hipEventDestroy.argtypes = [_P]
+            for fn in (hip.hipEventCreateWithFlags, hip.hipEventRecord, hip.hipEventElapsedTime,
+                       hip.hipEventDestroy):
+                fn.restype = ctypes.c_int
+            _hip = hip
+    return _hip
+
+
+def hip_check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with hipError_t {rc}")

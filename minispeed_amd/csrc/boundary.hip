@@ -18,8 +18,9 @@
 //
 // Everything here is HBM-bound streaming; no MFMA.  Work is cut into tiles
 // of consecutive flat indices.  In K3 and K4 a lane moves quads of 4
-// elements in wave order (see kStreamThreads); in K1 and K5 it owns groups
-// of kVec consecutive elements.  A tile (K3-K5) or a segment piece (K1) with
+// elements in wave order (see kStreamThreads), in K1 16-byte units of raw
+// gradient in wave order; in K5 it owns groups of kVec consecutive
+// elements.  A tile (K3-K5) or a segment piece (K1) with
 // suitably aligned storage takes the vector path; tiles that straddle
 // segment edges, partial tail tiles and misaligned segments take a
 // per-element path.
@@ -53,7 +54,7 @@ namespace {
 // K5: 2 wave64 per block, kVec consecutive elements per lane, one
 // 1024-element tile per block.
 constexpr int kThreads = 128;
-constexpr int kVec = 8;                   // elements per lane per tile (K1, K5)
+constexpr int kVec = 8;                   // K5: elements per lane; K1: chunk granule
 constexpr int kTile = kThreads * kVec;    // 1024 flat elements
 
 // K3 and K4 stream in "wave" order: a tile is kStreamThreads x kStreamUnroll
@@ -88,7 +89,7 @@ constexpr int kScanThreads = MS_SCAN_THREADS;   // K1 block: 8 wave64
 #ifndef MS_SCAN_DEPTH
 #define MS_SCAN_DEPTH 4
 #endif
-constexpr int kScanDepth = MS_SCAN_DEPTH;   // K1 vector groups in flight per lane
+constexpr int kScanDepth = MS_SCAN_DEPTH;   // K1: 16-byte units of gradient in flight per lane
 constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
 constexpr int kMaxSegs = 1 << 26;
 
@@ -169,21 +170,17 @@ __device__ inline void load_raw8(const void* p, typename D::raw (&r)[kVec]) {
   }
 }
 
-// kVec raw elements as 32-bit words (kVec*kBytes/4 of them), 16-byte aligned,
-// with the non-temporal hint (K1 reads each gradient once).
-template <class D>
-__device__ inline void load_words(const void* p, uint32_t (&w)[kVec * D::kBytes / 4]) {
-  const u4* q = reinterpret_cast<const u4*>(p);
+// 16 bytes of raw gradient (8 fp16 / bf16 or 4 fp32 elements), 16-byte
+// aligned, as four 32-bit words, with the non-temporal hint (K1 reads each
+// gradient once).
+__device__ inline void load_unit(const void* p, uint32_t (&w)[4]) {
+  const u4 x = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
 #pragma unroll
-  for (int j = 0; j < kVec * D::kBytes / 16; ++j) {
-    const u4 x = __builtin_nontemporal_load(q + j);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) w[4 * j + k] = x[k];
-  }
+  for (int k = 0; k < 4; ++k) w[k] = x[k];
 }
 
 template <class D>
-__device__ inline typename D::raw word_elem(const uint32_t (&w)[kVec * D::kBytes / 4], int k) {
+__device__ inline typename D::raw unit_elem(const uint32_t (&w)[4], int k) {
   if constexpr (D::kBytes == 2)
     return static_cast<uint16_t>((k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu));
   else
@@ -314,11 +311,11 @@ __device__ inline double wave_sum(double x) {
 // Block b of the grid (stats_grid(n) blocks) owns the contiguous flat
 // range [begin + b*chunk, begin + (b+1)*chunk), chunk a multiple of kVec,
 // and walks the segments inside it with a cursor.  Each piece of a segment
-// is a scalar head, a vector body of kVec-element groups (lane j of the
-// block takes groups j, j+256, ...) and a scalar tail.  Lanes accumulate
-// their own elements in index order, waves reduce with a fixed xor tree and
-// the four wave sums are added in wave order, so the per-block partials and
-// hence the norm are bitwise reproducible run to run.
+// is a scalar head, a vector body of 16-byte units (lane j of the block
+// takes units j, j + kScanThreads, ...) and a scalar tail.  Lanes
+// accumulate their own elements in index order, waves reduce with a fixed
+// xor tree and the wave sums are added in wave order, so the per-block
+// partials and hence the norm are bitwise reproducible run to run.
 template <class G, bool kFlat, bool kStats>
 struct GradScan {
   int umode;
@@ -343,58 +340,64 @@ struct GradScan {
     if (kFlat) flat[i - begin] = g;
   }
 
-  __device__ void group(const ms_segment_t& sg, const uint32_t (&w)[kVec * G::kBytes / 4],
-                        int64_t i, bool count) {
+  // One unit: the 16 bytes of raw gradient (kUnit consecutive elements,
+  // i .. i + kUnit - 1) a lane moves with one load, as four 32-bit words.
+  static constexpr int kUnit = 16 / G::kBytes;
+  __device__ void unit(const uint32_t (&w)[4], int64_t i, bool count) {
 #pragma unroll
-    for (int j = 0; j < kVec * G::kBytes / 4; ++j) packed |= (w[j] & G::kExp) + G::kExpOne;
-    float g[kVec];
+    for (int j = 0; j < 4; ++j) packed |= (w[j] & G::kExp) + G::kExpOne;
+    float g[kUnit];
 #pragma unroll
-    for (int k = 0; k < kVec; ++k) {
-      g[k] = unscale1(G::widen(word_elem<G>(w, k)), umode, scale, inv);
+    for (int k = 0; k < kUnit; ++k) {
+      g[k] = unscale1(G::widen(unit_elem<G>(w, k)), umode, scale, inv);
       if (kStats && count) {
         const double d = static_cast<double>(g[k]);
         acc = __builtin_fma(d, d, acc);
       }
     }
-    if (kFlat) store_f8(flat + (i - begin), g);
+    if (kFlat) {
+#pragma unroll
+      for (int k = 0; k < kUnit; k += 4)
+        *reinterpret_cast<f4*>(flat + (i - begin) + k) = f4{g[k], g[k + 1], g[k + 2], g[k + 3]};
+    }
   }
 
   // elements [a, b) of segment sg, all inside or all outside the owned range
   __device__ void piece(const ms_segment_t& sg, int64_t a, int64_t b, bool count, int lane) {
     const bool vec = sg.grad != nullptr && aligned16(sg.grad) &&
-                     (!kFlat || aligned16(flat)) && ((sg.begin - begin) & (kVec - 1)) == 0;
+                     (!kFlat || (aligned16(flat) && ((sg.begin - begin) & (kUnit - 1)) == 0));
     if (!vec) {
       if (!sg.grad && !kFlat) return;      // zeros: nothing to count or test
       for (int64_t i = a + lane; i < b; i += kScanThreads) element(sg, i, count);
       return;
     }
-    const int64_t a8 = sg.begin + (((a - sg.begin) + kVec - 1) & ~int64_t(kVec - 1));
-    const int64_t b8 = sg.begin + ((b - sg.begin) & ~int64_t(kVec - 1));
-    if (a8 >= b8) {
+    const int64_t au = sg.begin + (((a - sg.begin) + kUnit - 1) & ~int64_t(kUnit - 1));
+    const int64_t bu = sg.begin + ((b - sg.begin) & ~int64_t(kUnit - 1));
+    if (au >= bu) {
       for (int64_t i = a + lane; i < b; i += kScanThreads) element(sg, i, count);
       return;
     }
-    for (int64_t i = a + lane; i < a8; i += kScanThreads) element(sg, i, count);
-    for (int64_t i = b8 + lane; i < b; i += kScanThreads) element(sg, i, count);
-    const int64_t ng = (b8 - a8) / kVec;
-    const char* src = static_cast<const char*>(sg.grad) + (a8 - sg.begin) * G::kBytes;
-    // kScanDepth groups in flight per lane; each lane still takes its
-    // groups j, j + kScanThreads, ... in increasing order, so its running
-    // sum (and the block's partial) does not depend on the depth
-    constexpr int kWords = kVec * G::kBytes / 4;
-    int64_t j = lane;
-    for (; j + (kScanDepth - 1) * kScanThreads < ng; j += kScanDepth * kScanThreads) {
-      uint32_t w[kScanDepth][kWords];
+    for (int64_t i = a + lane; i < au; i += kScanThreads) element(sg, i, count);
+    for (int64_t i = bu + lane; i < b; i += kScanThreads) element(sg, i, count);
+    const int64_t nu = (bu - au) / kUnit;
+    const char* src = static_cast<const char*>(sg.grad) + (au - sg.begin) * G::kBytes;
+    // Wave order: lane j takes units j, j + kScanThreads, ..., so each load
+    // instruction of a wave reads one contiguous kilobyte of whole cache
+    // lines.  kScanDepth units are in flight per lane; each lane still takes
+    // its units in increasing order, so its running sum (and the block's
+    // partial) does not depend on the depth.
+    int64_t u = lane;
+    for (; u + (kScanDepth - 1) * kScanThreads < nu; u += kScanDepth * kScanThreads) {
+      uint32_t w[kScanDepth][4];
 #pragma unroll
-      for (int d = 0; d < kScanDepth; ++d)
-        load_words<G>(src + (j + d * kScanThreads) * (kVec * G::kBytes), w[d]);
+      for (int d = 0; d < kScanDepth; ++d) load_unit(src + (u + d * kScanThreads) * 16, w[d]);
 #pragma unroll
-      for (int d = 0; d < kScanDepth; ++d) group(sg, w[d], a8 + (j + d * kScanThreads) * kVec, count);
+      for (int d = 0; d < kScanDepth; ++d) unit(w[d], au + (u + d * kScanThreads) * kUnit, count);
     }
-    for (; j < ng; j += kScanThreads) {
-      uint32_t w0[kWords];
-      load_words<G>(src + j * (kVec * G::kBytes), w0);
-      group(sg, w0, a8 + j * kVec, count);
+    for (; u < nu; u += kScanThreads) {
+      uint32_t w0[4];
+      load_unit(src + u * 16, w0);
+      unit(w0, au + u * kUnit, count);
     }
   }
 };
