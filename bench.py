@@ -14,7 +14,10 @@ sets, resident in HBM, is re-attached to ``param.grad`` (what the last
 bracketed as a whole by ``torch.cuda.synchronize()``; ``ms_per_step`` is
 the bracket over K.  The same steps are then run one at a time, each
 bracketed on its own (``ms_per_step_synced``: the latency of one boundary,
-host work before the first kernel included).  A second, shorter run with
+host work before the first kernel included).  With ``--mode contiguous``
+the accumulation kernels of the gradient hooks (backward work on the same
+stream) run before every step, so its steps are only timed one at a time
+(``timing`` in the JSON line says which).  A second, shorter run with
 the masters and moments in separate allocations is reported next to the
 engine's default placement (``separate_allocations``).
 
@@ -45,12 +48,15 @@ if ROOT not in sys.path:
 
 METRIC = "boundary-step Gparams/s + HBM GB/s (% of peak) at 1.3B fp16, 1 GPU"
 PEAK_GBPS = 8000.0
-# HBM bytes per launch counted by two rocprofv3 --pmc runs (FETCH_SIZE x 2.0,
-# WRITE_SIZE x 1.0, both scales calibrated on a 1 GiB device copy in the same
-# runs); commands and per-kernel counts in profiles/traffic_gpt-1.3b_fp16.md
+# HBM bytes per launch counted by two rocprofv3 --pmc runs of this file's
+# default workload and layout (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, both scales
+# calibrated on a 1 GiB device copy in the same runs; mean of 7 launches);
+# commands and per-kernel counts in profiles/traffic_gpt-1.3b_fp16.md.  Keyed
+# by kernel / workload / grad dtype / mode / state window in GiB: a run in
+# any other configuration reports null.
 MEASURED_TRAFFIC = {
-    "k3/gpt-1.3b/fp16/fused/32.0": 36_841_000_000,
-    "k1/gpt-1.3b/fp16/fused/32.0": 2_635_000_000,
+    "k3/gpt-1.3b/fp16/fused/32.0": 36_840_555_520,
+    "k1/gpt-1.3b/fp16/fused/32.0": 2_715_717_924,
 }
 
 # algorithmic bytes per parameter: (K1, K3) for half / fp32 gradients
@@ -505,26 +511,32 @@ def main(argv=None) -> int:
         log(f"[bench] state placement {spacing!r}: window {window:g} GiB; warming up")
         gather_s, accum_s = [], []
 
-        def attach(k: int) -> None:
+        def attach(k: int, measure: bool = False) -> None:
             """What the last backward of a window leaves: grads on every param
-            (ZeRO-3: after the forward's parameter gather, timed on its own)."""
+            (ZeRO-3: after the forward's parameter gather; contiguous mode:
+            after the post-accumulate-grad hooks and their end-of-backward
+            flush).  With ``measure`` the gather and the hooks are timed on
+            their own, between synchronisations."""
             if args.zero_stage == 3:
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
+                if measure:
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
                 engine.optimizer.gather_parameters()
-                torch.cuda.synchronize()
-                gather_s.append(time.perf_counter() - t0)
+                if measure:
+                    torch.cuda.synchronize()
+                    gather_s.append(time.perf_counter() - t0)
             for p, g in zip(params, grad_sets[k % 2]):
                 p.grad = g
             if engine.contiguous is not None:
-                # what the post-accumulate-grad hooks do during the backward of a
-                # one-micro-batch window, timed on its own
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
+                if measure:
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
                 for i, p in enumerate(params):
                     engine.contiguous.accumulate(0, i, p)
-                torch.cuda.synchronize()
-                accum_s.append(time.perf_counter() - t0)
+                engine.contiguous.flush()
+                if measure:
+                    torch.cuda.synchronize()
+                    accum_s.append(time.perf_counter() - t0)
             engine.micro_steps += 1
 
         def boundary() -> None:
@@ -540,31 +552,44 @@ def main(argv=None) -> int:
         # 2 events per kernel launch (K1 and K3 per group, K2 once), created
         # before the timed loop
         timer = LaunchTimer(reserve=2 * (2 * len(engine.flat_groups) + 1) * steps)
-        engine.optimizer.launch_timer = timer if kernel_timing else None
-        # the timed steps, bracketed as a whole: each step re-attaches its
-        # gradients (what the window's last backward leaves) and runs the
-        # boundary; the host work of step k+1 overlaps K3 of step k
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(steps):
-            attach(k)
-            boundary()                       # ends with the one scalar read-back
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        engine.optimizer.launch_timer = None
+        # Contiguous mode: the hooks' accumulation kernels are backward work
+        # on the same stream, so its boundaries are timed one at a time (the
+        # second loop) and the kernel events go there.
+        back_to_back = engine.contiguous is None
+        elapsed = None
+        if back_to_back:
+            # the timed steps, bracketed as a whole: each step re-attaches its
+            # gradients (what the window's last backward leaves) and runs the
+            # boundary; the host work of step k+1 overlaps K3 of step k
+            engine.optimizer.launch_timer = timer if kernel_timing else None
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for k in range(steps):
+                attach(k)
+                boundary()                       # ends with the one scalar read-back
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - t0
+            engine.optimizer.launch_timer = None
         # the same steps one at a time, each bracketed by synchronisations: the
         # latency of one boundary, host work before K1 included
         step_s = []
         for k in range(steps):
-            attach(k)
+            attach(k, measure=True)
+            if not back_to_back:
+                engine.optimizer.launch_timer = timer if kernel_timing else None
             torch.cuda.synchronize()
             t1 = time.perf_counter()
             boundary()
             torch.cuda.synchronize()
             step_s.append(time.perf_counter() - t1)
-        log(f"[bench] {steps} boundary steps: {elapsed * 1e3:.3f} ms back to back, "
+            engine.optimizer.launch_timer = None
+        if elapsed is None:
+            elapsed = sum(step_s)
+        log(f"[bench] {steps} boundary steps: {elapsed * 1e3:.3f} ms "
+            f"{'back to back' if back_to_back else 'one at a time'}, "
             f"{sum(step_s) * 1e3:.3f} ms one at a time")
         out = {"ms_step": elapsed / steps * 1e3, "step_s": step_s, "window_gib": window,
+               "timing": "back to back" if back_to_back else "one at a time",
                "k_ms": ({k: float(np.mean(timer.durations_ms(k))) for k in ("k1", "k2", "k3")}
                         if kernel_timing else None)}
         if accum_s:
@@ -616,6 +641,7 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "timing": head["timing"],
         "ms_per_step_synced": round(float(np.mean(head["step_s"])) * 1e3, 4),
         "ms_per_step_synced_median": round(float(np.median(head["step_s"])) * 1e3, 4),
         "higher_is_better": True,

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MS_ABI_VERSION 4
+#define MS_ABI_VERSION 5
 
 /* groups one ms_boundary_scalars_noalloc call can scan (its static scratch:
  * MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() partial slots of 12 bytes) */
@@ -239,6 +239,32 @@ int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,
  */
 int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n,
                        int32_t first, void* stream);
+
+/* One gradient of a batched K5 call: dst [dev] fp32, src [dev] of the
+ * call's src_dtype, numel elements; first != 0 overwrites dst. */
+typedef struct ms_accum_row {
+  float* dst;
+  const void* src;
+  int64_t numel;
+  int32_t first;
+  int32_t reserved;   /* 0 */
+} ms_accum_row_t;     /* 32 bytes */
+
+/* Rows per K5 launch of ms_accumulate_grads (they travel in the kernel
+ * arguments, so a batch needs no device-side table). */
+#define MS_ACCUM_ROWS_PER_LAUNCH 64
+
+/*
+ * K5, batched: ms_accumulate_grad for every row of rows[0 .. nrows) [host
+ * memory, read before the call returns], ceil(nrows / 64) launches.  Rows
+ * with numel 0 are skipped; the dst ranges of one call must not overlap.
+ * The contiguous-gradient hooks queue the gradients backward produces and
+ * flush them through this call (at the end of backward, or when a bucket
+ * fills), in place of one launch per parameter per micro-batch; same
+ * reference lines as ms_accumulate_grad.
+ */
+int ms_accumulate_grads(const ms_accum_row_t* rows, int32_t nrows, int32_t src_dtype,
+                        void* stream);
 
 /* One group's part of ms_boundary_scalars_noalloc: the arguments
  * ms_grad_stats takes for it. */

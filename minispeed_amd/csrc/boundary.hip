@@ -17,10 +17,9 @@
 //                     into its flat slice (contiguous gradients)
 //
 // Everything here is HBM-bound streaming; no MFMA.  Work is cut into tiles
-// of consecutive flat indices.  In K3 and K4 a lane moves quads of 4
+// of consecutive flat indices.  In K3, K4 and K5 a lane moves quads of 4
 // elements in wave order (see kStreamThreads), in K1 16-byte units of raw
-// gradient in wave order; in K5 it owns groups of kVec consecutive
-// elements.  A tile (K3-K5) or a segment piece (K1) with
+// gradient in wave order.  A tile (K3-K5) or a segment piece (K1) with
 // suitably aligned storage takes the vector path; tiles that straddle
 // segment edges, partial tail tiles and misaligned segments take a
 // per-element path.
@@ -51,13 +50,10 @@ static __device__ __align__(256) unsigned char scratch[MS_SCRATCH_MAX_GROUPS * k
 
 namespace {
 
-// K5: 2 wave64 per block, kVec consecutive elements per lane, one
-// 1024-element tile per block.
-constexpr int kThreads = 128;
-constexpr int kVec = 8;                   // K5: elements per lane; K1: chunk granule
-constexpr int kTile = kThreads * kVec;    // 1024 flat elements
+// K1 block ranges are multiples of kVec elements.
+constexpr int kVec = 8;
 
-// K3 and K4 stream in "wave" order: a tile is kStreamThreads x kStreamUnroll
+// K3, K4 and K5 stream in "wave" order: a tile is kStreamThreads x kStreamUnroll
 // quads of 4 consecutive elements, and quad u of lane j is quad
 // u * kStreamThreads + j, so every load or store instruction of a wave
 // covers one contiguous run (64 x 16 bytes of fp32) and every cache line it
@@ -148,28 +144,6 @@ struct DBF16 {
   }
 };
 
-// Load / store kVec consecutive raw elements at a 16-byte aligned address
-// (K5's per-parameter gradient reads), with the non-temporal hint.
-template <class D>
-__device__ inline void load_raw8(const void* p, typename D::raw (&r)[kVec]) {
-  if constexpr (D::kBytes == 2) {
-    u4 w = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      r[2 * k] = static_cast<uint16_t>(w[k] & 0xffffu);
-      r[2 * k + 1] = static_cast<uint16_t>(w[k] >> 16);
-    }
-  } else {
-    const u4* q = reinterpret_cast<const u4*>(p);
-    u4 a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      r[k] = a[k];
-      r[4 + k] = b[k];
-    }
-  }
-}
-
 // 16 bytes of raw gradient (8 fp16 / bf16 or 4 fp32 elements), 16-byte
 // aligned, as four 32-bit words, with the non-temporal hint (K1 reads each
 // gradient once).
@@ -185,28 +159,6 @@ __device__ inline typename D::raw unit_elem(const uint32_t (&w)[4], int k) {
     return static_cast<uint16_t>((k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu));
   else
     return w[k];
-}
-
-__device__ inline void load_f8(const float* p, float (&x)[kVec]) {
-  const f4* q = reinterpret_cast<const f4*>(p);
-  f4 a = q[0], b = q[1];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    x[k] = a[k];
-    x[4 + k] = b[k];
-  }
-}
-
-__device__ inline void store_f8(float* p, const float (&x)[kVec]) {
-  f4* q = reinterpret_cast<f4*>(p);
-  f4 a, b;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    a[k] = x[k];
-    b[k] = x[4 + k];
-  }
-  q[0] = a;
-  q[1] = b;
 }
 
 // A quad: 4 consecutive elements, 16 bytes of fp32 or 8 of fp16 / bf16, at an
@@ -720,38 +672,76 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
 }
 
 // ------------------------------------------------------------------ K5
-// dst[i] = (first ? 0 : dst[i]) + widen(src[i]) over one parameter's flat
-// slice, i in [0, n): one fp32 rounding per add, as torch's fp32 add_ of a
-// widened tensor.  The vector path needs both addresses 16-byte aligned;
-// otherwise every lane steps element by element.
+// dst[i] = (first ? 0 : dst[i]) + widen(src[i]) over the flat slices of up
+// to kAccumRows gradients: one fp32 rounding per add, as torch's fp32 add_
+// of a widened tensor.  The rows travel by value in the kernel arguments
+// (about 2 KB), so a batch needs no table in device memory.  Block t works
+// on tile t of the concatenated rows: row r owns tiles [tile0[r],
+// tile0[r+1]), each of kStreamTile elements in wave order, with the
+// non-temporal hint (the accumulation buffer and the gradient are each
+// touched once per micro-batch).  A tile whose addresses are not quad
+// aligned, or the last partial tile of a row, steps element by element.
+constexpr int kAccumRows = MS_ACCUM_ROWS_PER_LAUNCH;
+
+struct AccumLaunch {
+  int64_t tile0[kAccumRows + 1];   // tile0[nrows] = tiles of the launch
+  float* dst[kAccumRows];
+  const void* src[kAccumRows];
+  int64_t numel[kAccumRows];
+  uint64_t first;                  // bit r: row r overwrites dst
+  int32_t nrows;
+};
+static_assert(kAccumRows <= 64, "one bit of AccumLaunch::first per row");
+static_assert(sizeof(AccumLaunch) <= 4096, "K5 rows must fit in the kernel arguments");
+static_assert(sizeof(ms_accum_row_t) == 32, "ms_accum_row_t layout");
+
 template <class D>
-__global__ __launch_bounds__(kThreads) void k_accumulate(
-    float* __restrict__ dst, const void* __restrict__ src, int64_t n, int first) {
-  const bool vec = aligned16(dst) && aligned16(src);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  int64_t done = 0;
-  if (vec) {
-    const int64_t nvec = n / kVec;
-    for (int64_t c = tid; c < nvec; c += stride) {
-      typename D::raw r[kVec];
-      load_raw8<D>(static_cast<const char*>(src) + c * kVec * D::kBytes, r);
-      float x[kVec];
-      if (first) {
-#pragma unroll
-        for (int k = 0; k < kVec; ++k) x[k] = D::widen(r[k]);
-      } else {
-        load_f8(dst + c * kVec, x);
-#pragma unroll
-        for (int k = 0; k < kVec; ++k) x[k] = x[k] + D::widen(r[k]);
-      }
-      store_f8(dst + c * kVec, x);
+__global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch L) {
+  const int lane = threadIdx.x;
+  const int64_t ntiles = L.tile0[L.nrows];
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    // the last row starting at or before t: rows with no tiles share their
+    // tile0 with the next row, so this row holds t
+    int lo = 0, hi = L.nrows - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (L.tile0[mid] <= t)
+        lo = mid;
+      else
+        hi = mid - 1;
     }
-    done = nvec * kVec;
-  }
-  for (int64_t i = done + tid; i < n; i += stride) {
-    const float g = D::widen(load_raw1<D>(src, i));
-    dst[i] = first ? g : dst[i] + g;
+    const int r = lo;
+    float* __restrict__ dst = L.dst[r];
+    const char* __restrict__ src = static_cast<const char*>(L.src[r]);
+    const int64_t n = L.numel[r];
+    const bool first = ((L.first >> r) & 1u) != 0;
+    const int64_t e0 = (t - L.tile0[r]) * kStreamTile;
+    const int64_t e1 = (e0 + kStreamTile < n) ? e0 + kStreamTile : n;
+    if (e1 - e0 == kStreamTile && quad_aligned(dst, e0, 4) && quad_aligned(src, e0, D::kBytes)) {
+      float g[kStreamUnroll][4], x[kStreamUnroll][4];
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t i = e0 + static_cast<int64_t>(u * kStreamThreads + lane) * 4;
+        ldq_raw<D>(src + i * D::kBytes, g[u]);
+        if (!first) ldq(dst + i, x[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t i = e0 + static_cast<int64_t>(u * kStreamThreads + lane) * 4;
+        if (first) {
+          stq(dst + i, g[u]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) x[u][k] = x[u][k] + g[u][k];
+          stq(dst + i, x[u]);
+        }
+      }
+    } else {
+      for (int64_t i = e0 + lane; i < e1; i += kStreamThreads) {
+        const float g1 = D::widen(load_raw1<D>(src, i));
+        dst[i] = first ? g1 : dst[i] + g1;
+      }
+    }
   }
 }
 
@@ -1067,27 +1057,60 @@ int ms_fused_adamw(float* master, float* exp_avg, float* exp_avg_sq,
   return launch_status();
 }
 
+int ms_accumulate_grads(const ms_accum_row_t* rows, int32_t nrows, int32_t src_dtype,
+                        void* stream) {
+  if (!valid_dtype(src_dtype) || nrows < 0 || (nrows > 0 && !rows)) return MS_EINVAL;
+  for (int32_t r = 0; r < nrows; ++r) {
+    if (rows[r].numel < 0 || (rows[r].numel > 0 && (!rows[r].dst || !rows[r].src)))
+      return MS_EINVAL;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  AccumLaunch L;
+  int32_t r = 0;
+  while (r < nrows) {
+    // the next launch: up to kAccumRows rows with elements
+    L.nrows = 0;
+    L.first = 0;
+    int64_t tiles = 0;
+    for (; r < nrows && L.nrows < kAccumRows; ++r) {
+      const ms_accum_row_t& row = rows[r];
+      if (row.numel == 0) continue;
+      const int k = L.nrows++;
+      L.tile0[k] = tiles;
+      L.dst[k] = row.dst;
+      L.src[k] = row.src;
+      L.numel[k] = row.numel;
+      if (row.first) L.first |= uint64_t(1) << k;
+      tiles += (row.numel + kStreamTile - 1) / kStreamTile;
+    }
+    if (L.nrows == 0) break;
+    L.tile0[L.nrows] = tiles;
+    const dim3 grid(stream_grid(tiles));
+    const dim3 block(kStreamThreads);
+    switch (src_dtype) {
+      case MS_DTYPE_F32:
+        hipLaunchKernelGGL(k_accumulate<DF32>, grid, block, 0, st, L);
+        break;
+      case MS_DTYPE_F16:
+        hipLaunchKernelGGL(k_accumulate<DF16>, grid, block, 0, st, L);
+        break;
+      default:
+        hipLaunchKernelGGL(k_accumulate<DBF16>, grid, block, 0, st, L);
+        break;
+    }
+    const int rc = launch_status();
+    if (rc != MS_OK) return rc;
+  }
+  return MS_OK;
+}
+
 int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n,
                        int32_t first, void* stream) {
   if (!valid_dtype(src_dtype) || n < 0) return MS_EINVAL;
   if (n == 0) return MS_OK;
   if (!dst || !src) return MS_EINVAL;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(stream_grid((n + kTile - 1) / kTile));
-  const dim3 block(kThreads);
-  const int f = first ? 1 : 0;
-  switch (src_dtype) {
-    case MS_DTYPE_F32:
-      hipLaunchKernelGGL(k_accumulate<DF32>, grid, block, 0, st, dst, src, n, f);
-      break;
-    case MS_DTYPE_F16:
-      hipLaunchKernelGGL(k_accumulate<DF16>, grid, block, 0, st, dst, src, n, f);
-      break;
-    default:
-      hipLaunchKernelGGL(k_accumulate<DBF16>, grid, block, 0, st, dst, src, n, f);
-      break;
-  }
-  return launch_status();
+  const ms_accum_row_t row{dst, src, n, first ? 1 : 0, 0};
+  return ms_accumulate_grads(&row, 1, src_dtype, stream);
 }
 
 int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,

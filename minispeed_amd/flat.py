@@ -696,17 +696,21 @@ class FlatParamGroup:
         """Every gradient widened exactly into its parameter's slice of one
         fp32 buffer (the opt-in accumulation kernel with ``first`` set):
         addresses into it, the tensors to keep, and ``MS_DTYPE_F32``."""
+        from .contiguous import ACCUM_ROW, accumulate_rows
         buf = torch.empty(self.numel, dtype=torch.float32, device=self.device)
         base = buf.data_ptr()
         ptrs = np.zeros(len(self.params) + 1, dtype=np.int64)
-        lib = _native.load()
-        stream = _native.stream_handle(self.device)
+        by_dtype = {}
         for k, (g, off, n) in enumerate(zip(grads, self.layout.offsets, self._numels)):
             if g is None or n == 0:
                 continue
-            _native.check(lib.ms_accumulate_grad(base + 4 * off, g.data_ptr(), _native.ms_dtype(g.dtype),
-                                                 n, 1, stream), "ms_accumulate_grad(widen)")
+            by_dtype.setdefault(g.dtype, []).append((base + 4 * off, g.data_ptr(), n))
             ptrs[k] = base + 4 * off
+        for dtype, items in by_dtype.items():
+            rows = np.zeros(len(items), dtype=ACCUM_ROW)
+            rows["dst"], rows["src"], rows["numel"] = zip(*items)
+            rows["first"] = 1
+            accumulate_rows(rows, _native.ms_dtype(dtype), self.device)
         return ptrs, [*grads, buf], _native.DTYPE_F32
 
     def model_pointers(self) -> np.ndarray:

@@ -1,8 +1,9 @@
 """Opt-in contiguous gradients on the GPU.
 
-* K5 (``ms_accumulate_grad``) against the fp32 sum of widened gradients,
-  bit for bit, for every dtype, aligned and misaligned slices, ragged sizes,
-  inf/nan;
+* K5 (``ms_accumulate_grad``, and batched, ``ms_accumulate_grads``: 150
+  rows, three launches) against the fp32 sum of widened gradients, bit for
+  bit, for every dtype, aligned and misaligned slices, ragged sizes,
+  inf/nan; the elements between the slices stay untouched;
 * the engine in this mode against the oracle's boundary given the fp32 sums
   (bit-exact flags, scale and Adam moments when the clip coefficients agree;
   masters within 2 fp32 ulp per step; norm within 1e-5), through real
@@ -10,7 +11,8 @@
 * where half-precision accumulation is exact the mode equals the default
   mode bit for bit; parameters without a gradient in a window count as
   zeros; an overflow skips the step and the next window starts clean;
-  ZeRO-3 equals ZeRO-0.
+  ZeRO-3 equals ZeRO-0; flushing the queued gradients inside backward (a
+  bucket of one element) equals one flush at the end of backward.
 """
 
 from __future__ import annotations
@@ -55,6 +57,48 @@ def test_accumulate_kernel_is_the_fp32_sum(dtype, n, off):
         assert torch.equal(torch.isnan(got), torch.isnan(want))
     # the guard elements around the slice are untouched
     assert torch.all(buf[:off].cpu() == -3.0) and torch.all(buf[off + n:].cpu() == -3.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_batched_accumulation_is_the_fp32_sum_of_every_row(dtype):
+    """150 rows (three launches of 64 / 64 / 22) of ragged sizes, dst slices
+    at every alignment with 3 guard elements between them, some sources one
+    element off their alignment, first / add mixed within a launch."""
+    from minispeed_amd.contiguous import ACCUM_ROW, accumulate_rows
+    rng = np.random.default_rng(7)
+    sizes = rng.choice([0, 1, 3, 4, 2047, 2048, 2049, 4101, 10000], size=150)
+    shifts = rng.integers(0, 4, size=150)          # dst start mod 4
+    pos, p = [], 8
+    for n, sh in zip(sizes, shifts):
+        p += (-p + sh) % 4
+        pos.append(p)
+        p += int(n) + 3
+    buf = torch.full((p + 8,), -3.0, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    want = [None] * len(sizes)
+    for rnd in range(3):
+        srcs, rows = [], np.zeros(len(sizes), dtype=ACCUM_ROW)
+        for r, n in enumerate(sizes):
+            off = int(rng.integers(0, 2)) if rnd else 0
+            x = torch.randn(int(n) + off, generator=gen, device=DEV).to(dtype)[off:]
+            if n > 100 and rnd == 1 and r % 7 == 0:
+                x[17] = float("inf")
+                x[40] = float("nan")
+            srcs.append(x)
+            first = rnd == 0 or (rnd == 2 and r % 5 == 0)
+            rows[r] = (buf.data_ptr() + 4 * pos[r], x.data_ptr(), int(n), 1 if first else 0, 0)
+            want[r] = ob.accumulate_fp32(None if first else want[r], x.cpu())
+        accumulate_rows(rows, _native.ms_dtype(dtype), torch.device(DEV))
+        host = buf.cpu()
+        for r, n in enumerate(sizes):
+            got, w = host[pos[r]:pos[r] + int(n)], want[r]
+            ok = ~torch.isnan(w)
+            assert torch.equal(got.view(torch.int32)[ok], w.view(torch.int32)[ok]), (rnd, r)
+            assert torch.equal(torch.isnan(got), torch.isnan(w)), (rnd, r)
+        touched = torch.zeros(len(host), dtype=torch.bool)
+        for r, n in enumerate(sizes):
+            touched[pos[r]:pos[r] + int(n)] = True
+        assert torch.all(host[~touched] == -3.0), rnd
 
 
 def test_accumulate_kernel_rejects_bad_arguments():
@@ -103,11 +147,13 @@ def _coeffs(seed, dyadic):
     return out
 
 
-def _run(dtype, stage, contiguous, windows, dyadic, skip_at=None, inf_at=None, gas=2):
+def _run(dtype, stage, contiguous, windows, dyadic, skip_at=None, inf_at=None, gas=2, bucket=None):
     torch.manual_seed(0)
     model = Linear({"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dtype]).to(DEV)
     engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
                            config=_cfg(dtype, stage, contiguous, gas))
+    if bucket is not None:
+        engine.contiguous.bucket_elements = bucket
     applied = []
     for w in range(windows):
         for m in range(gas):
@@ -148,6 +194,15 @@ def test_overflow_skips_and_the_next_window_starts_clean():
     assert ra == rb and rb.count(True) == 2 and b.skipped_steps == 1
     assert a.get_loss_scale() == b.get_loss_scale() == 2.0 ** 7
     assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
+
+
+def test_flushes_inside_backward_equal_one_flush_at_its_end():
+    a, _, ra = _run("bf16", 0, True, 3, dyadic=False, gas=3)
+    b, _, rb = _run("bf16", 0, True, 3, dyadic=False, gas=3, bucket=1)
+    assert ra == rb
+    assert a.grad_norm == b.grad_norm
+    assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
+    assert torch.equal(a.optimizer.state[0]["exp_avg_sq"], b.optimizer.state[0]["exp_avg_sq"])
 
 
 def test_stage3_equals_stage0():

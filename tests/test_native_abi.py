@@ -64,6 +64,10 @@ int main(void) {
   F(ms_group_scan_t, segs) F(ms_group_scan_t, nseg) F(ms_group_scan_t, grad_dtype)
   F(ms_group_scan_t, begin) F(ms_group_scan_t, end) F(ms_group_scan_t, own_begin)
   F(ms_group_scan_t, own_end)
+  printf("ms_accum_row_t %zu\n", sizeof(ms_accum_row_t));
+  F(ms_accum_row_t, dst) F(ms_accum_row_t, src) F(ms_accum_row_t, numel) F(ms_accum_row_t, first)
+  F(ms_accum_row_t, reserved)
+  printf("MS_ACCUM_ROWS_PER_LAUNCH %d\n", MS_ACCUM_ROWS_PER_LAUNCH);
   printf("MS_SCRATCH_MAX_GROUPS %d\n", MS_SCRATCH_MAX_GROUPS);
   printf("MS_ESCRATCH %d\n", MS_ESCRATCH);
   return 0;
@@ -74,7 +78,9 @@ int main(void) {
     lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
     got = dict(line.rsplit(" ", 1) for line in lines if line)
     classes = {"ms_segment_t": _native.Segment, "ms_step_scalars_t": _native.StepScalars,
-               "ms_adamw_params_t": _native.AdamWParams, "ms_group_scan_t": _native.GroupScan}
+               "ms_adamw_params_t": _native.AdamWParams, "ms_group_scan_t": _native.GroupScan,
+               "ms_accum_row_t": _native.AccumRow}
+    assert int(got.pop("MS_ACCUM_ROWS_PER_LAUNCH")) == _native.ACCUM_ROWS_PER_LAUNCH
     assert int(got.pop("MS_SCRATCH_MAX_GROUPS")) == _native.SCRATCH_MAX_GROUPS
     assert int(got.pop("MS_ESCRATCH")) == _native.ESCRATCH
     for key, value in got.items():
@@ -132,6 +138,22 @@ def test_host_argument_errors_return_codes_without_launching():
     assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == EINVAL
     scans[0] = _native.GroupScan(None, 0, 1, 0, 10, 0, 10)
     assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == ETABLE
+    # batched K5: dtype, row count, a NULL row array, a negative size, a
+    # missing address; empty rows launch nothing
+    rows = (_native.AccumRow * 3)()
+    acc = lib.ms_accumulate_grads
+    assert acc(rows, 3, 5, None) == EINVAL
+    assert acc(rows, -1, 1, None) == EINVAL
+    assert acc(None, 1, 1, None) == EINVAL
+    assert acc(None, 0, 1, None) == 0
+    assert acc(rows, 3, 1, None) == 0                   # three rows of numel 0
+    rows[1] = _native.AccumRow(8, 8, -1, 1, 0)
+    assert acc(rows, 3, 1, None) == EINVAL
+    rows[1] = _native.AccumRow(None, 8, 10, 1, 0)
+    assert acc(rows, 3, 1, None) == EINVAL
+    assert lib.ms_accumulate_grad(None, None, 1, 0, 1, None) == 0
+    assert lib.ms_accumulate_grad(None, 8, 1, 10, 1, None) == EINVAL
+    assert lib.ms_accumulate_grad(8, 8, 4, 10, 1, None) == EINVAL
     for code in (0, EINVAL, ETABLE, EBLOCKS, _native.ESCRATCH):
         assert lib.ms_error_string(code)
     with pytest.raises(RuntimeError, match="segment count"):
