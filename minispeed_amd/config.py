@@ -33,11 +33,12 @@ it is not bitwise minispeed and is off by default.
 groups: with a number of GiB they are views of one allocation (the state
 arena) of three windows of that size, array j at the start of window j; 0
 gives three separate allocations; "auto" (the default) uses 32 GiB windows
-for states of 1 to 32 GiB per array when the 96 GiB arena takes at most
-half of the free device memory, and separate allocations otherwise.  On
-MI355X the arena makes the fused AdamW kernel 10-15% faster than separate
-allocations (1.3B params: 5.7-6.1 against 6.5-6.9 ms), at the price of the
-windows' unused part (about 80 GiB at 1.3B params, 6 GiB at 8B).  The
+for states of 256 MiB to 32 GiB per array when the 96 GiB arena takes at
+most half of the free device memory, and separate allocations otherwise.
+On MI355X the arena makes the fused AdamW kernel 10-15% faster than
+separate allocations (1.3B params: 5.7-5.9 against 6.5-6.9 ms; 124M params:
+0.54 against 0.61-0.63 ms), at the price of the windows' unused part (about
+80 GiB at 1.3B params, 6 GiB at 8B).  The
 placement changes no result.  The tensors are then views of one
 allocation: ``torch.save`` them through ``state_dict()`` / the checkpoint
 functions (which copy them out), not directly.

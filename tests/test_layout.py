@@ -167,7 +167,7 @@ def test_state_arena_layout():
     assert starts == [[0, 32 << 30, 64 << 30]] and total == 96 << 30
 
 
-def test_auto_window_is_32_gib_for_states_of_1_to_32_gib_per_array():
+def test_auto_window_is_32_gib_for_states_of_256_mib_to_32_gib_per_array():
     from minispeed_amd.flat import auto_window
 
     gib = 1 << 30
@@ -176,6 +176,9 @@ def test_auto_window_is_32_gib_for_states_of_1_to_32_gib_per_array():
     n8 = 8_030_261_248                                        # Llama-3-8B whole: 29.9 GiB
     assert auto_window([[n8, n8, n8]]) == 32 * gib
     assert auto_window([[3_323_392] * 3]) == 0                # tiny LM: 13 MB arrays
+    assert auto_window([[124_439_808] * 3]) == 32 * gib       # GPT-2 small: 0.46 GiB arrays
+    assert auto_window([[(256 << 20) // 4] * 3]) == 32 * gib  # exactly 256 MiB
+    assert auto_window([[(256 << 20) // 4 - (1 << 20)] * 3]) == 0    # 252 MiB
     assert auto_window([[n8 + n13] * 3]) == 0                 # 35 GiB: separate
     assert auto_window([[n13, n13, n13], [n13, n13, n13]]) == 32 * gib     # 9.8 GiB columns
     assert auto_window([]) == 0
