@@ -29,11 +29,12 @@ import numpy as np
 import torch
 
 from . import _native
-from .flat import FlatParamGroup
+from .flat import FlatParamGroup, record_streams
 
 
 def _f32(x: float) -> float:
-    return float(np.float32(x))
+    """x rounded to fp32 (round to nearest even), as a Python float."""
+    return ctypes.c_float(x).value
 
 
 def adamw_params(
@@ -42,24 +43,26 @@ def adamw_params(
 ) -> _native.AdamWParams:
     """Round this step's AdamW scalars the way the torch op sequence of
     optim/adam.py:72-91 does: every Python double becomes fp32 at the op that
-    consumes it."""
+    consumes it.  The doubles are computed here and stored into the
+    ``c_float`` fields of the struct, a C double -> float conversion that
+    rounds to nearest even, as ``np.float32`` does."""
     lr = float(lr)
     beta1, beta2 = (float(b) for b in betas)
     wd = float(weight_decay)
-    hp = _native.AdamWParams()
-    hp.neg_lr = _f32(-lr)
-    hp.decay_alpha = _f32(-lr * wd)
-    hp.beta1 = _f32(beta1)
-    hp.one_minus_beta1 = _f32(1.0 - beta1)
-    hp.beta2 = _f32(beta2)
-    hp.one_minus_beta2 = _f32(1.0 - beta2)
-    hp.bias_c1 = _f32(1.0 - beta1 ** step)
-    hp.bias_c2 = _f32(1.0 - beta2 ** step)
-    hp.eps = _f32(float(eps))
-    hp.grad_scale = _f32(grad_scale)
-    hp.decay = 1 if wd != 0.0 else 0
-    hp.unscale = _native.SCALE_DIVIDE if unscale else _native.SCALE_NONE
-    return hp
+    return _native.AdamWParams(
+        neg_lr=-lr,
+        decay_alpha=-lr * wd,
+        beta1=beta1,
+        one_minus_beta1=1.0 - beta1,
+        beta2=beta2,
+        one_minus_beta2=1.0 - beta2,
+        bias_c1=1.0 - beta1 ** step,
+        bias_c2=1.0 - beta2 ** step,
+        eps=float(eps),
+        grad_scale=float(grad_scale),
+        decay=1 if wd != 0.0 else 0,
+        unscale=_native.SCALE_DIVIDE if unscale else _native.SCALE_NONE,
+    )
 
 
 class Workspace:
@@ -315,9 +318,7 @@ def run_boundary(
     # memory to that stream while K1 / K3 still read it here.  Recording
     # this stream on them defers the reuse until everything queued here so
     # far has run.  Done while K1 / K2 run, before the host waits.
-    for t in keep:
-        if t is not None:
-            t.record_stream(cur)
+    record_streams(keep, cur)
     return ws.finish_readback()
 
 

@@ -39,7 +39,7 @@ import numpy as np
 import torch
 
 from . import _native
-from .flat import FlatParamGroup
+from .flat import FlatParamGroup, record_streams
 
 
 # K5's row layout (ms_accum_row_t) as a numpy record
@@ -143,9 +143,7 @@ class ContiguousGradients:
             accumulate_rows(rows, _native.ms_dtype(dtype), device)
             # the gradients' memory goes back to the caching allocator, which
             # hands it out again only in the order of this stream
-            stream = torch.cuda.current_stream(device)
-            for _, _, grad, _ in items:
-                grad.record_stream(stream)
+            record_streams([grad for _, _, grad, _ in items], torch.cuda.current_stream(device))
 
     def grad_pointers(self, gi: int) -> np.ndarray:
         """Addresses of the fp32 sums of group ``gi`` (0 for parameters

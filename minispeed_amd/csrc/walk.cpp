@@ -16,6 +16,8 @@
 #include <torch/csrc/utils/pybind.h>
 #include <pybind11/numpy.h>
 
+#include <c10/core/Stream.h>
+
 #include <cstdint>
 
 namespace py = pybind11;
@@ -90,10 +92,36 @@ int64_t model_pointers(py::list params, int64_t device_index,
   return -1;
 }
 
+// record_streams(tensors, device_type, device_index, stream_id) -> count
+//   Tensor.record_stream(stream) for every device tensor of `tensors` (None
+//   entries and host tensors are skipped): the caching allocator then hands
+//   their memory out again only after the work queued on that stream by the
+//   time they are freed.  One call instead of one Python call per tensor
+//   (~0.3 us each) at every boundary.
+int64_t record_streams(py::list tensors, int64_t device_type, int64_t device_index,
+                       int64_t stream_id) {
+  const c10::Stream stream(c10::Stream::UNSAFE,
+                           c10::Device(static_cast<c10::DeviceType>(device_type),
+                                       static_cast<c10::DeviceIndex>(device_index)),
+                           static_cast<c10::StreamId>(stream_id));
+  int64_t count = 0;
+  const Py_ssize_t n = PyList_GET_SIZE(tensors.ptr());
+  for (Py_ssize_t k = 0; k < n; ++k) {
+    PyObject* obj = PyList_GET_ITEM(tensors.ptr(), k);
+    if (obj == Py_None) continue;
+    const at::Tensor t = unpack(obj);
+    if (!t.is_cuda()) continue;
+    t.record_stream(stream);
+    ++count;
+  }
+  return count;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_walk, m) {
   m.doc() = "device addresses of parameter gradients / storages for the boundary tables";
   m.def("grad_pointers", &grad_pointers);
   m.def("model_pointers", &model_pointers);
+  m.def("record_streams", &record_streams);
 }

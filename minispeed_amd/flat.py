@@ -57,6 +57,14 @@ def _walk():
     return mod
 
 
+def record_streams(tensors: Sequence[Optional[torch.Tensor]], stream: torch.cuda.Stream) -> None:
+    """``t.record_stream(stream)`` for every device tensor of ``tensors``
+    (``None`` entries skipped), in one call into the C++ walk."""
+    items = tensors if isinstance(tensors, list) else list(tensors)
+    _walk().record_streams(items, int(stream.device_type), int(stream.device_index),
+                           int(stream.stream_id))
+
+
 def _with_pad_slot(ptrs, n_params: int) -> np.ndarray:
     """Addresses as int64 with a trailing 0 for the padding row."""
     if isinstance(ptrs, np.ndarray) and ptrs.shape == (n_params + 1,):
@@ -834,9 +842,7 @@ class FlatParamGroup:
         self.release_grads()
         # the gradients may have been allocated on another stream: their
         # memory must not be reused there before the kernel above has read it
-        cur = torch.cuda.current_stream(self.device)
-        for g in keep:
-            g.record_stream(cur)
+        record_streams(keep, torch.cuda.current_stream(self.device))
         del keep
 
     @torch.no_grad()

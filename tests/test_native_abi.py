@@ -195,3 +195,8 @@ def test_pointer_walk_extension_loads_and_defers_host_tensors():
     assert _walk.model_pointers(params, 0, out) == 0
     with pytest.raises(ValueError):
         _walk.grad_pointers(params, np.array([3], dtype=np.int64), 0, out)
+    # record_streams skips None and host tensors (nothing to record) and
+    # refuses what is not a tensor
+    assert _walk.record_streams([None, torch.zeros(2), params[0]], 1, 0, 0) == 0
+    with pytest.raises(TypeError):
+        _walk.record_streams([3], 1, 0, 0)
