@@ -44,7 +44,10 @@
 // uint32 flags.  Host code never names this array directly (its host-side
 // name is not a device address): it uses the per-device address from
 // hipGetSymbolAddress (scratch_base below).
-constexpr int kStatsBlocksFixed = 16384;
+#ifndef MS_STATS_BLOCKS
+#define MS_STATS_BLOCKS 16384
+#endif
+constexpr int kStatsBlocksFixed = MS_STATS_BLOCKS;
 static __device__ __align__(256) unsigned char scratch[MS_SCRATCH_MAX_GROUPS * kStatsBlocksFixed *
                                                        (sizeof(double) + sizeof(uint32_t))];
 
