@@ -56,9 +56,10 @@ namespace {
 // K1 block ranges are multiples of kVec elements.
 constexpr int kVec = 8;
 
-// K3, K4 and K5 stream in "wave" order: a tile is kStreamThreads x kStreamUnroll
-// quads of 4 consecutive elements, and quad u of lane j is quad
-// u * kStreamThreads + j, so every load or store instruction of a wave
+// K3, K4 and K5 stream in "wave" order: a tile is T x U quads of 4
+// consecutive elements (T threads, U quads per lane; kStreamThreads x
+// kStreamUnroll for K4 and K5, kAdamThreads x kAdamUnroll for K3), and quad u
+// of lane j is quad u * T + j, so every load or store instruction of a wave
 // covers one contiguous run (64 x 16 bytes of fp32) and every cache line it
 // touches is whole.  That is what lets every stream carry the non-temporal
 // hint: with 8 consecutive elements per lane a store instruction writes
@@ -71,7 +72,20 @@ constexpr int kVec = 8;
 #endif
 constexpr int kStreamThreads = MS_STREAM_THREADS;
 constexpr int kStreamUnroll = MS_STREAM_UNROLL;
-constexpr int kStreamTile = kStreamThreads * kStreamUnroll * 4;   // 2048 flat elements
+constexpr int kStreamTile = kStreamThreads * kStreamUnroll * 4;   // 2048 flat elements (K4, K5)
+// K3's own shape: one quad per lane, 512-element tiles.  Over the 1.3B
+// state its K3 takes 5.77 ms against 5.79 ms with K4's 256 x 2 (the
+// shard and the contiguous mode gain 1.5%), while K4 and K5 are 25-33%
+// slower with K3's shape.
+#ifndef MS_ADAM_THREADS
+#define MS_ADAM_THREADS 128
+#endif
+#ifndef MS_ADAM_UNROLL
+#define MS_ADAM_UNROLL 1
+#endif
+constexpr int kAdamThreads = MS_ADAM_THREADS;
+constexpr int kAdamUnroll = MS_ADAM_UNROLL;
+constexpr int kAdamTile = kAdamThreads * kAdamUnroll * 4;          // 512 flat elements (K3)
 constexpr int kStatsBlocks = kStatsBlocksFixed;   // K1 partial slots per group
 #ifndef MS_STATS_MIN_CHUNK
 #define MS_STATS_MIN_CHUNK 32768
@@ -540,14 +554,14 @@ __device__ inline void adamw1(float g, float& p, float& m, float& v,
   p = p + (h.neg_lr * (m / h.bc1)) / den;
 }
 
-// One block per kStreamTile-element tile (grid-stride when the grid is
+// One block per kAdamTile-element tile (grid-stride when the grid is
 // clamped).  A tile inside one segment whose grad / model addresses are
-// quad-aligned takes the vector path: each lane streams kStreamUnroll quads
+// quad-aligned takes the vector path: each lane streams kAdamUnroll quads
 // in wave order, all loads of the tile first, then the arithmetic and all
 // stores.  Other tiles (segment edges, the tail, misaligned storage) go
-// element by element: lane j takes elements j, j + kStreamThreads, ...
+// element by element: lane j takes elements j, j + kAdamThreads, ...
 template <class G, class M, bool kFlatGrad>
-__global__ __launch_bounds__(kStreamThreads) void k_adamw(
+__global__ __launch_bounds__(kAdamThreads) void k_adamw(
     float* __restrict__ master, float* __restrict__ exp_avg,
     float* __restrict__ exp_avg_sq, const float* __restrict__ flat_grad,
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
@@ -557,26 +571,26 @@ __global__ __launch_bounds__(kStreamThreads) void k_adamw(
   const float coef = sc->coef;
   const int lane = threadIdx.x;
   const int64_t n = end - begin;
-  const int64_t ntiles = (n + kStreamTile - 1) / kStreamTile;
+  const int64_t ntiles = (n + kAdamTile - 1) / kAdamTile;
   const bool arrays_vec = aligned16(master) && aligned16(exp_avg) &&
                           aligned16(exp_avg_sq) &&
                           (!kFlatGrad || aligned16(flat_grad));
 
   for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    const int64_t t0 = begin + t * kStreamTile;
-    const int64_t t1 = (t0 + kStreamTile < end) ? t0 + kStreamTile : end;
+    const int64_t t0 = begin + t * kAdamTile;
+    const int64_t t1 = (t0 + kAdamTile < end) ? t0 + kAdamTile : end;
     const int s = find_seg(segs, nseg, t0);
     const ms_segment_t seg = segs[s];
     const int64_t so = t0 - seg.begin;   // the tile's offset in the segment
-    const bool fast = t1 - t0 == kStreamTile && so >= 0 && t1 <= seg_end(seg) && arrays_vec &&
+    const bool fast = t1 - t0 == kAdamTile && so >= 0 && t1 <= seg_end(seg) && arrays_vec &&
                       (kFlatGrad || seg.grad == nullptr || quad_aligned(seg.grad, so, G::kBytes)) &&
                       (seg.model == nullptr || quad_aligned(seg.model, so, M::kBytes));
     if (fast) {
       const int64_t tl = t0 - begin;     // the tile's offset in the state arrays
-      float g[kStreamUnroll][4], p[kStreamUnroll][4], m[kStreamUnroll][4], v[kStreamUnroll][4];
+      float g[kAdamUnroll][4], p[kAdamUnroll][4], m[kAdamUnroll][4], v[kAdamUnroll][4];
 #pragma unroll
-      for (int u = 0; u < kStreamUnroll; ++u) {
-        const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
+      for (int u = 0; u < kAdamUnroll; ++u) {
+        const int64_t e = 4 * (static_cast<int64_t>(u) * kAdamThreads + lane);
         if (kFlatGrad) {
           ldq(flat_grad + tl + e, g[u]);
         } else if (seg.grad) {
@@ -590,8 +604,8 @@ __global__ __launch_bounds__(kStreamThreads) void k_adamw(
         ldq(exp_avg_sq + tl + e, v[u]);
       }
 #pragma unroll
-      for (int u = 0; u < kStreamUnroll; ++u) {
-        const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
+      for (int u = 0; u < kAdamUnroll; ++u) {
+        const int64_t e = 4 * (static_cast<int64_t>(u) * kAdamThreads + lane);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           if (!kFlatGrad && seg.grad) g[u][k] = unscale1(g[u][k], h.umode, h.grad_scale, h.inv_scale);
@@ -604,8 +618,8 @@ __global__ __launch_bounds__(kStreamThreads) void k_adamw(
       }
     } else {
       int sl = s;
-      for (int k = 0; k < 4 * kStreamUnroll; ++k) {
-        const int64_t i = t0 + lane + static_cast<int64_t>(k) * kStreamThreads;
+      for (int k = 0; k < 4 * kAdamUnroll; ++k) {
+        const int64_t i = t0 + lane + static_cast<int64_t>(k) * kAdamThreads;
         if (i >= t1) break;
         while (sl + 1 < nseg && i >= seg_end(segs[sl])) ++sl;
         const ms_segment_t& sg = segs[sl];
@@ -887,9 +901,9 @@ void launch_adamw(float* p, float* m, float* v, const float* fg,
                   const ms_segment_t* segs, int nseg, int64_t begin, int64_t end,
                   const AdamScalars& h, const ms_step_scalars_t* sc,
                   hipStream_t st) {
-  const int64_t ntiles = (end - begin + kStreamTile - 1) / kStreamTile;
+  const int64_t ntiles = (end - begin + kAdamTile - 1) / kAdamTile;
   const dim3 grid(stream_grid(ntiles));
-  const dim3 block(kStreamThreads);
+  const dim3 block(kAdamThreads);
   if (fg)
     hipLaunchKernelGGL((k_adamw<G, M, true>), grid, block, 0, st, p, m, v, fg,
                        segs, nseg, begin, end, h, sc);
