@@ -261,15 +261,10 @@ class SegmentTable:
 _ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
 
 
-def _flat_view(t: torch.Tensor) -> torch.Tensor:
-    return t if t.is_contiguous() else t.contiguous()
-
-
 # State placement (``hip_boundary.state_spacing_gib``): AUTO_SPACING picks
 # the window from the state's size (``auto_window``), 0 means separate
 # allocations, a positive value is the window in bytes.
 AUTO_SPACING = -1
-STATE_SPACING_BYTES = 32 << 30       # the window the 8B-param states need
 _AUTO_WINDOW = 32 << 30
 _AUTO_MIN_COLUMN = 256 << 20   # the Infinity Cache: smaller states stay cache resident
 _AUTO_MAX_SHARE = 0.5      # of the free device memory
