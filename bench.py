@@ -65,8 +65,11 @@ BYTES = {
     ("materialize", 2): (6, 30),   # K1 read g2 write f4 | K3 read f4+12, write 12+2
     ("fused", 4): (4, 32),
     ("materialize", 4): (8, 32),
-    ("contiguous", 2): (4, 30),    # K1 read fp32 sum 4 | K3 read 4+12, write 12+2
-    ("contiguous", 4): (4, 30),
+    # contiguous: the accumulation kernel leaves the tile statistics, so the
+    # boundary folds them (12 B per 2048 params) instead of a K1 read of the
+    # fp32 sums | K3 read 4+12, write 12+2
+    ("contiguous", 2): (0, 30),
+    ("contiguous", 4): (0, 30),
 }
 
 

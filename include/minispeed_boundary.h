@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MS_ABI_VERSION 5
+#define MS_ABI_VERSION 6
 
 /* groups one ms_boundary_scalars_noalloc call can scan (its static scratch:
  * MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() partial slots of 12 bytes) */
@@ -241,18 +241,28 @@ int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n
                        int32_t first, void* stream);
 
 /* One gradient of a batched K5 call: dst [dev] fp32, src [dev] of the
- * call's src_dtype, numel elements; first != 0 overwrites dst. */
+ * call's src_dtype, numel elements; first != 0 overwrites dst.
+ * tile_sumsq / tile_flag [dev, optional, both or neither]: one slot per
+ * MS_ACCUM_TILE elements of dst (ceil(numel / MS_ACCUM_TILE) slots); K5
+ * writes each tile's fp64 sum of squares of the NEW dst values, unscaled
+ * as ms_grad_stats unscales (the call's unscale / grad_scale), and a flag
+ * that is non-zero iff one of those values is inf/nan (tested before
+ * unscaling). */
 typedef struct ms_accum_row {
   float* dst;
   const void* src;
   int64_t numel;
   int32_t first;
-  int32_t reserved;   /* 0 */
-} ms_accum_row_t;     /* 32 bytes */
+  int32_t reserved;     /* 0 */
+  double* tile_sumsq;
+  uint32_t* tile_flag;
+} ms_accum_row_t;       /* 48 bytes */
 
 /* Rows per K5 launch of ms_accumulate_grads (they travel in the kernel
- * arguments, so a batch needs no device-side table). */
+ * arguments, so a batch needs no device-side table), and the elements one
+ * K5 tile (one statistics slot) covers. */
 #define MS_ACCUM_ROWS_PER_LAUNCH 64
+#define MS_ACCUM_TILE 2048
 
 /*
  * K5, batched: ms_accumulate_grad for every row of rows[0 .. nrows) [host
@@ -261,10 +271,27 @@ typedef struct ms_accum_row {
  * The contiguous-gradient hooks queue the gradients backward produces and
  * flush them through this call (at the end of backward, or when a bucket
  * fills), in place of one launch per parameter per micro-batch; same
- * reference lines as ms_accumulate_grad.
+ * reference lines as ms_accumulate_grad.  With tile statistics the same
+ * pass also does the work of the boundary scan (K1) over the new sums:
+ * the flag and per-tile sum of squares of flat.py:196-257 and
+ * stage_1_and_2.py:105-116, which ms_reduce_tile_stats then folds into
+ * ms_norm_clip's partial slots.  unscale: MS_SCALE_NONE or
+ * MS_SCALE_DIVIDE (grad_scale > 0).
  */
 int ms_accumulate_grads(const ms_accum_row_t* rows, int32_t nrows, int32_t src_dtype,
-                        void* stream);
+                        int32_t unscale, float grad_scale, void* stream);
+
+/*
+ * Fold per-tile statistics (K5's tile_sumsq / tile_flag of one group,
+ * ntiles slots [dev]) into the nblk >= ms_stats_blocks() partial slots
+ * ms_norm_clip reads for that group [dev]: slot j holds the fp64 sum, in
+ * slot order, of tiles [j*ntiles/nblk, (j+1)*ntiles/nblk) and the OR of
+ * their flags, so the norm is a pure function of the tile statistics.
+ * Replaces K1 (ms_grad_stats) at a contiguous-gradient boundary.
+ */
+int ms_reduce_tile_stats(const double* tile_sumsq, const uint32_t* tile_flag, int64_t ntiles,
+                         double* block_sumsq, uint32_t* block_flag, int32_t nblk,
+                         void* stream);
 
 /* One group's part of ms_boundary_scalars_noalloc: the arguments
  * ms_grad_stats takes for it. */

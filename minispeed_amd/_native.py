@@ -19,7 +19,7 @@ from typing import Optional
 import torch  # noqa: F401  (must precede the dlopen below, see module doc)
 
 LIB_NAME = "libminispeed_boundary.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -110,10 +110,13 @@ class AccumRow(ctypes.Structure):
         ("numel", ctypes.c_int64),
         ("first", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("tile_sumsq", ctypes.c_void_p),
+        ("tile_flag", ctypes.c_void_p),
     ]
 
 
 ACCUM_ROWS_PER_LAUNCH = 64
+ACCUM_TILE = 2048
 
 SEGMENT_BYTES = ctypes.sizeof(Segment)
 SCALARS_BYTES = ctypes.sizeof(StepScalars)
@@ -143,7 +146,8 @@ SIGNATURES = {
     ),
     "ms_cast_to_model": (ctypes.c_int, [_P, _I64, _I64, _P, _I32, _I32, _P]),
     "ms_accumulate_grad": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _P]),
-    "ms_accumulate_grads": (ctypes.c_int, [_P, _I32, _I32, _P]),
+    "ms_accumulate_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _F, _P]),
+    "ms_reduce_tile_stats": (ctypes.c_int, [_P, _P, _I64, _P, _P, _I32, _P]),
     "ms_boundary_scalars_noalloc": (
         ctypes.c_int,
         [ctypes.POINTER(GroupScan), _I32, _I32, _F, _I32, _D, _I32, _D, _I64, _I64, _I64, _D, _D,

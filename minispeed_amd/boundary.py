@@ -23,7 +23,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import Callable, List, Optional, Sequence
+from typing import Callable, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -213,6 +213,9 @@ class GroupLaunch:
     exp_avg_sq: torch.Tensor
     grads: Sequence[int]          # gradient address per parameter (0: none)
     grad_dtype: Optional[int] = None   # MS_DTYPE_* of the gradients (default: the params')
+    # (sum-of-squares slots, flag slots, count) K5 left for the gradients
+    # (contiguous mode): folded into the partial sums instead of the K1 scan
+    tile_stats: Optional[Tuple[int, int, int]] = None
 
 
 def run_boundary(
@@ -262,17 +265,26 @@ def run_boundary(
             g._grad_dirty = True
         lo, hi = g.own_range
         gbytes = 4 if gdtype == _native.DTYPE_F32 else 2
-        t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None, gbytes), cur)
         psum, pflag = ws.partial_ptrs(gi)
-        tok = timer.start("k1")
-        rc = lib.ms_grad_stats(
-            t1[0], t1[1], gdtype, 0, g.numel_padded, lo, hi,
-            _native.SCALE_DIVIDE if unscale else _native.SCALE_NONE, scale32,
-            flat_out.data_ptr() if flat_out is not None else None,
-            psum, pflag, ws.nblk, stream,
-        )
-        timer.stop(tok)
-        _native.check(rc, "ms_grad_stats")
+        if gl.tile_stats is not None and flat_out is None and (lo, hi) == (0, g.numel_padded):
+            # the accumulation pass already scanned the sums: fold its tile
+            # statistics into the partial slots (no second read of the sums)
+            ts, tf, ntiles = gl.tile_stats
+            tok = timer.start("k1")
+            rc = lib.ms_reduce_tile_stats(ts or None, tf or None, ntiles, psum, pflag, ws.nblk, stream)
+            timer.stop(tok)
+            _native.check(rc, "ms_reduce_tile_stats")
+        else:
+            t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None, gbytes), cur)
+            tok = timer.start("k1")
+            rc = lib.ms_grad_stats(
+                t1[0], t1[1], gdtype, 0, g.numel_padded, lo, hi,
+                _native.SCALE_DIVIDE if unscale else _native.SCALE_NONE, scale32,
+                flat_out.data_ptr() if flat_out is not None else None,
+                psum, pflag, ws.nblk, stream,
+            )
+            timer.stop(tok)
+            _native.check(rc, "ms_grad_stats")
         dtypes.append((gdtype, dtype, gbytes))
         flats.append(flat_out)
 

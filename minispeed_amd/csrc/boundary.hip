@@ -692,28 +692,41 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
 // dst[i] = (first ? 0 : dst[i]) + widen(src[i]) over the flat slices of up
 // to kAccumRows gradients: one fp32 rounding per add, as torch's fp32 add_
 // of a widened tensor.  The rows travel by value in the kernel arguments
-// (about 2 KB), so a batch needs no table in device memory.  Block t works
+// (about 3 KB), so a batch needs no table in device memory.  Block t works
 // on tile t of the concatenated rows: row r owns tiles [tile0[r],
 // tile0[r+1]), each of kStreamTile elements in wave order, with the
 // non-temporal hint (the accumulation buffer and the gradient are each
 // touched once per micro-batch).  A tile whose addresses are not quad
 // aligned, or the last partial tile of a row, steps element by element.
+// With statistics slots (ps / pf of the row) the block also writes the
+// tile's fp64 sum of squares of the unscaled new values (each lane adds
+// its own values in index order, waves reduce with a fixed xor tree, the
+// wave sums are added in wave order: bitwise reproducible) and whether any
+// new value is inf/nan.
 constexpr int kAccumRows = MS_ACCUM_ROWS_PER_LAUNCH;
+static_assert(kStreamTile == MS_ACCUM_TILE, "a K5 tile is one statistics slot");
 
 struct AccumLaunch {
   int64_t tile0[kAccumRows + 1];   // tile0[nrows] = tiles of the launch
   float* dst[kAccumRows];
   const void* src[kAccumRows];
   int64_t numel[kAccumRows];
+  double* ps[kAccumRows];          // per-tile sum of squares, or null
+  uint32_t* pf[kAccumRows];        // per-tile inf/nan flag, or null
   uint64_t first;                  // bit r: row r overwrites dst
   int32_t nrows;
+  int32_t umode;                   // unscale1 mode of the statistics
+  float scale, inv;
 };
 static_assert(kAccumRows <= 64, "one bit of AccumLaunch::first per row");
 static_assert(sizeof(AccumLaunch) <= 4096, "K5 rows must fit in the kernel arguments");
-static_assert(sizeof(ms_accum_row_t) == 32, "ms_accum_row_t layout");
+static_assert(sizeof(ms_accum_row_t) == 48, "ms_accum_row_t layout");
 
 template <class D>
 __global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch L) {
+  constexpr int kWaves = kStreamThreads / 64;
+  __shared__ double wsum[kWaves];
+  __shared__ uint32_t wbad[kWaves];
   const int lane = threadIdx.x;
   const int64_t ntiles = L.tile0[L.nrows];
   for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
@@ -732,8 +745,17 @@ __global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch
     const char* __restrict__ src = static_cast<const char*>(L.src[r]);
     const int64_t n = L.numel[r];
     const bool first = ((L.first >> r) & 1u) != 0;
-    const int64_t e0 = (t - L.tile0[r]) * kStreamTile;
+    const bool stats = L.ps[r] != nullptr;
+    const int64_t tile = t - L.tile0[r];
+    const int64_t e0 = tile * kStreamTile;
     const int64_t e1 = (e0 + kStreamTile < n) ? e0 + kStreamTile : n;
+    double acc = 0.0;
+    bool bad = false;
+    auto count = [&](float x) {
+      bad |= (__float_as_uint(x) & 0x7f800000u) == 0x7f800000u;
+      const double d = static_cast<double>(unscale1(x, L.umode, L.scale, L.inv));
+      acc = __builtin_fma(d, d, acc);
+    };
     if (e1 - e0 == kStreamTile && quad_aligned(dst, e0, 4) && quad_aligned(src, e0, D::kBytes)) {
       float g[kStreamUnroll][4], x[kStreamUnroll][4];
 #pragma unroll
@@ -745,21 +767,67 @@ __global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
         const int64_t i = e0 + static_cast<int64_t>(u * kStreamThreads + lane) * 4;
-        if (first) {
-          stq(dst + i, g[u]);
-        } else {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) x[u][k] = x[u][k] + g[u][k];
-          stq(dst + i, x[u]);
+        for (int k = 0; k < 4; ++k) x[u][k] = first ? g[u][k] : x[u][k] + g[u][k];
+        stq(dst + i, x[u]);
+        if (stats) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) count(x[u][k]);
         }
       }
     } else {
       for (int64_t i = e0 + lane; i < e1; i += kStreamThreads) {
         const float g1 = D::widen(load_raw1<D>(src, i));
-        dst[i] = first ? g1 : dst[i] + g1;
+        const float x1 = first ? g1 : dst[i] + g1;
+        dst[i] = x1;
+        if (stats) count(x1);
       }
     }
+    if (stats) {   // uniform over the block: one tile, one row
+      const double w = wave_sum(acc);
+      const bool wb = __any(bad);
+      if ((lane & 63) == 0) {
+        wsum[lane >> 6] = w;
+        wbad[lane >> 6] = wb ? 1u : 0u;
+      }
+      __syncthreads();
+      if (lane == 0) {
+        double total = 0.0;
+        uint32_t flag = 0;
+#pragma unroll
+        for (int k = 0; k < kWaves; ++k) {
+          total += wsum[k];
+          flag |= wbad[k];
+        }
+        L.ps[r][tile] = total;
+        L.pf[r][tile] = flag;
+      }
+      __syncthreads();   // wsum / wbad are reused by the next tile
+    }
   }
+}
+
+// ------------------------------------------------------------------ K2a
+// Thread j folds tiles [j*ntiles/nblk, (j+1)*ntiles/nblk) into partial slot
+// j, in tile order: a fixed partition and order, so the result is a pure
+// function of the tile statistics.
+constexpr int kFoldThreads = 256;
+
+__global__ __launch_bounds__(kFoldThreads) void k_fold_tiles(
+    const double* __restrict__ ts, const uint32_t* __restrict__ tf, int64_t ntiles,
+    double* __restrict__ bsum, uint32_t* __restrict__ bflag, int nblk) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * kFoldThreads + threadIdx.x;
+  if (j >= nblk) return;
+  const int64_t lo = j * ntiles / nblk;
+  const int64_t hi = (j + 1) * ntiles / nblk;
+  double total = 0.0;
+  uint32_t flag = 0;
+  for (int64_t k = lo; k < hi; ++k) {
+    total += ts[k];
+    flag |= tf[k];
+  }
+  bsum[j] = total;
+  bflag[j] = flag ? 1u : 0u;
 }
 
 // ------------------------------------------------------------- launching
@@ -1075,14 +1143,21 @@ int ms_fused_adamw(float* master, float* exp_avg, float* exp_avg_sq,
 }
 
 int ms_accumulate_grads(const ms_accum_row_t* rows, int32_t nrows, int32_t src_dtype,
-                        void* stream) {
+                        int32_t unscale, float grad_scale, void* stream) {
   if (!valid_dtype(src_dtype) || nrows < 0 || (nrows > 0 && !rows)) return MS_EINVAL;
+  if (unscale != MS_SCALE_NONE && unscale != MS_SCALE_DIVIDE) return MS_EINVAL;
+  if (unscale == MS_SCALE_DIVIDE && !(grad_scale > 0.0f)) return MS_EINVAL;
   for (int32_t r = 0; r < nrows; ++r) {
-    if (rows[r].numel < 0 || (rows[r].numel > 0 && (!rows[r].dst || !rows[r].src)))
-      return MS_EINVAL;
+    const ms_accum_row_t& row = rows[r];
+    if (row.numel < 0 || (row.numel > 0 && (!row.dst || !row.src))) return MS_EINVAL;
+    if ((row.tile_sumsq == nullptr) != (row.tile_flag == nullptr)) return MS_EINVAL;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   AccumLaunch L;
+  float inv = 1.0f;
+  L.umode = unscale_mode(unscale, grad_scale, &inv);
+  L.scale = grad_scale;
+  L.inv = inv;
   int32_t r = 0;
   while (r < nrows) {
     // the next launch: up to kAccumRows rows with elements
@@ -1097,6 +1172,8 @@ int ms_accumulate_grads(const ms_accum_row_t* rows, int32_t nrows, int32_t src_d
       L.dst[k] = row.dst;
       L.src[k] = row.src;
       L.numel[k] = row.numel;
+      L.ps[k] = row.tile_sumsq;
+      L.pf[k] = row.tile_flag;
       if (row.first) L.first |= uint64_t(1) << k;
       tiles += (row.numel + kStreamTile - 1) / kStreamTile;
     }
@@ -1121,13 +1198,26 @@ int ms_accumulate_grads(const ms_accum_row_t* rows, int32_t nrows, int32_t src_d
   return MS_OK;
 }
 
+int ms_reduce_tile_stats(const double* tile_sumsq, const uint32_t* tile_flag, int64_t ntiles,
+                         double* block_sumsq, uint32_t* block_flag, int32_t nblk,
+                         void* stream) {
+  if (ntiles < 0 || !block_sumsq || !block_flag) return MS_EINVAL;
+  if (ntiles > 0 && (!tile_sumsq || !tile_flag)) return MS_EINVAL;
+  if (nblk < kStatsBlocks) return MS_EBLOCKS;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((nblk + kFoldThreads - 1) / kFoldThreads);
+  hipLaunchKernelGGL(k_fold_tiles, grid, dim3(kFoldThreads), 0, st, tile_sumsq, tile_flag,
+                     ntiles, block_sumsq, block_flag, nblk);
+  return launch_status();
+}
+
 int ms_accumulate_grad(float* dst, const void* src, int32_t src_dtype, int64_t n,
                        int32_t first, void* stream) {
   if (!valid_dtype(src_dtype) || n < 0) return MS_EINVAL;
   if (n == 0) return MS_OK;
   if (!dst || !src) return MS_EINVAL;
-  const ms_accum_row_t row{dst, src, n, first ? 1 : 0, 0};
-  return ms_accumulate_grads(&row, 1, src_dtype, stream);
+  const ms_accum_row_t row{dst, src, n, first ? 1 : 0, 0, nullptr, nullptr};
+  return ms_accumulate_grads(&row, 1, src_dtype, MS_SCALE_NONE, 1.0f, stream);
 }
 
 int ms_cast_to_model(const float* flat, int64_t begin, int64_t end,

@@ -111,7 +111,8 @@ class DeepSpeedEngine:
         self.optimizer = build_zero_optimizer(self.flat_groups, option_groups, zero_stage=self.config.zero_stage)
         self.contiguous: Optional[ContiguousGradients] = None
         if self.config.contiguous_gradients:
-            self.contiguous = ContiguousGradients(self.flat_groups)
+            self.contiguous = ContiguousGradients(
+                self.flat_groups, scale_fn=lambda: self.loss_scaler.loss_scale_factor)
             self.optimizer.contiguous = self.contiguous
         self.lr_scheduler = build_scheduler(
             self.optimizer, self.config.scheduler_type, self.config.scheduler_params

@@ -133,8 +133,10 @@ class ZeROOptimizer:
         for gi, (g, group, state) in enumerate(zip(self.flat_groups, self.adam.param_groups,
                                                    self.adam.state)):
             grad_dtype = None
+            tile_stats = None
             if self.contiguous is not None:
                 ptrs, grad_dtype = self.contiguous.grad_pointers(gi), _native.DTYPE_F32
+                tile_stats = self.contiguous.tile_stats(gi, scaler.loss_scale_factor)
             else:
                 ptrs, tensors, grad_dtype = g.grad_pointers()
                 keep.extend(tensors)
@@ -142,7 +144,7 @@ class ZeROOptimizer:
             launches.append(GroupLaunch(
                 group=g, lr=lr, betas=betas, eps=eps, weight_decay=wd,
                 step=state["step"] + 1, exp_avg=state["exp_avg"], exp_avg_sq=state["exp_avg_sq"],
-                grads=ptrs, grad_dtype=grad_dtype,
+                grads=ptrs, grad_dtype=grad_dtype, tile_stats=tile_stats,
             ))
 
         def model_targets():

@@ -12,7 +12,11 @@
   mode bit for bit; parameters without a gradient in a window count as
   zeros; an overflow skips the step and the next window starts clean;
   ZeRO-3 equals ZeRO-0; flushing the queued gradients inside backward (a
-  bucket of one element) equals one flush at the end of backward.
+  bucket of one element) equals one flush at the end of backward;
+* the boundary from K5's tile statistics (``ms_reduce_tile_stats``, checked
+  on its own against in-order fp64 sums) against the boundary that scans
+  the sums again, and the fall-back to that scan when the loss scale
+  changed inside a window.
 """
 
 from __future__ import annotations
@@ -59,11 +63,14 @@ def test_accumulate_kernel_is_the_fp32_sum(dtype, n, off):
     assert torch.all(buf[:off].cpu() == -3.0) and torch.all(buf[off + n:].cpu() == -3.0)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_batched_accumulation_is_the_fp32_sum_of_every_row(dtype):
+@pytest.mark.parametrize("dtype,scale_value", [(torch.float16, 1024.0), (torch.bfloat16, 1000.0),
+                                               (torch.float32, 3.0)])
+def test_batched_accumulation_is_the_fp32_sum_of_every_row(dtype, scale_value):
     """150 rows (three launches of 64 / 64 / 22) of ragged sizes, dst slices
     at every alignment with 3 guard elements between them, some sources one
-    element off their alignment, first / add mixed within a launch."""
+    element off their alignment, first / add mixed within a launch; the
+    tile statistics of the new sums against fp64 on the CPU (power-of-two
+    and IEEE-division unscaling), rows without slots leave them alone."""
     from minispeed_amd.contiguous import ACCUM_ROW, accumulate_rows
     rng = np.random.default_rng(7)
     sizes = rng.choice([0, 1, 3, 4, 2047, 2048, 2049, 4101, 10000], size=150)
@@ -76,6 +83,11 @@ def test_batched_accumulation_is_the_fp32_sum_of_every_row(dtype):
     buf = torch.full((p + 8,), -3.0, device=DEV)
     gen = torch.Generator(device=DEV).manual_seed(11)
     want = [None] * len(sizes)
+    tiles = [(int(n) + 2047) // 2048 for n in sizes]
+    t0 = np.concatenate([[0], np.cumsum(tiles)[:-1]]).astype(np.int64)
+    ts = torch.empty(max(1, sum(tiles)), dtype=torch.float64, device=DEV)
+    tf = torch.empty(max(1, sum(tiles)), dtype=torch.int32, device=DEV)
+    unscale, scale = _native.SCALE_DIVIDE, scale_value
     for rnd in range(3):
         srcs, rows = [], np.zeros(len(sizes), dtype=ACCUM_ROW)
         for r, n in enumerate(sizes):
@@ -86,19 +98,64 @@ def test_batched_accumulation_is_the_fp32_sum_of_every_row(dtype):
                 x[40] = float("nan")
             srcs.append(x)
             first = rnd == 0 or (rnd == 2 and r % 5 == 0)
-            rows[r] = (buf.data_ptr() + 4 * pos[r], x.data_ptr(), int(n), 1 if first else 0, 0)
+            stats = r % 3 != 2                      # some rows without statistics slots
+            rows[r] = (buf.data_ptr() + 4 * pos[r], x.data_ptr(), int(n), 1 if first else 0, 0,
+                       ts.data_ptr() + 8 * t0[r] if stats else 0,
+                       tf.data_ptr() + 4 * t0[r] if stats else 0)
             want[r] = ob.accumulate_fp32(None if first else want[r], x.cpu())
-        accumulate_rows(rows, _native.ms_dtype(dtype), torch.device(DEV))
-        host = buf.cpu()
+        ts.fill_(-1.0)
+        tf.fill_(-1)
+        accumulate_rows(rows, _native.ms_dtype(dtype), torch.device(DEV), unscale, scale)
+        host, hts, htf = buf.cpu(), ts.cpu().numpy(), tf.cpu().numpy()
         for r, n in enumerate(sizes):
             got, w = host[pos[r]:pos[r] + int(n)], want[r]
             ok = ~torch.isnan(w)
             assert torch.equal(got.view(torch.int32)[ok], w.view(torch.int32)[ok]), (rnd, r)
             assert torch.equal(torch.isnan(got), torch.isnan(w)), (rnd, r)
+            # per 2048-element tile: fp64 sum of squares of the unscaled new
+            # sums (the boundary scan's unscale) and the inf/nan flag
+            for k in range(tiles[r]):
+                seg = w[k * 2048:(k + 1) * 2048]
+                slot = t0[r] + k
+                if r % 3 == 2:
+                    assert hts[slot] == -1.0 and htf[slot] == -1, (rnd, r, k)   # untouched
+                    continue
+                bad = not bool(torch.isfinite(seg).all())
+                assert (htf[slot] != 0) == bad, (rnd, r, k)
+                if not bad:
+                    u = (seg / np.float32(scale)) if unscale else seg
+                    ref = float(np.sum(u.double().numpy() ** 2))
+                    assert abs(hts[slot] - ref) <= 1e-12 * ref, (rnd, r, k, hts[slot], ref)
         touched = torch.zeros(len(host), dtype=torch.bool)
         for r, n in enumerate(sizes):
             touched[pos[r]:pos[r] + int(n)] = True
         assert torch.all(host[~touched] == -3.0), rnd
+
+
+def test_folding_tile_statistics_sums_fixed_ranges_in_order():
+    """ms_reduce_tile_stats: slot j is the in-order fp64 sum of tiles
+    [j*T/nb, (j+1)*T/nb) and the OR of their flags, every slot written."""
+    lib = _native.load()
+    nb = _native.stats_blocks()
+    stream = _native.stream_handle(torch.device(DEV))
+    rng = np.random.default_rng(5)
+    for ntiles in (0, 1, 7, nb - 3, nb, 100_003):
+        ts_h = rng.standard_normal(ntiles) ** 2 * 10.0 ** rng.integers(-8, 8, ntiles)
+        tf_h = (rng.random(ntiles) < 0.001).astype(np.int32)
+        ts = torch.from_numpy(ts_h).to(DEV)
+        tf = torch.from_numpy(tf_h).to(DEV)
+        bs = torch.full((nb,), -1.0, dtype=torch.float64, device=DEV)
+        bf = torch.full((nb,), 7, dtype=torch.int32, device=DEV)
+        _native.check(lib.ms_reduce_tile_stats(ts.data_ptr() if ntiles else None,
+                                               tf.data_ptr() if ntiles else None, ntiles,
+                                               bs.data_ptr(), bf.data_ptr(), nb, stream),
+                      "ms_reduce_tile_stats")
+        got_s, got_f = bs.cpu().numpy(), bf.cpu().numpy()
+        for j in range(nb):
+            lo, hi = j * ntiles // nb, (j + 1) * ntiles // nb
+            want = np.cumsum(ts_h[lo:hi])[-1] if hi > lo else 0.0
+            assert got_s[j] == want, (ntiles, j)
+            assert got_f[j] == (1 if tf_h[lo:hi].any() else 0), (ntiles, j)
 
 
 def test_accumulate_kernel_rejects_bad_arguments():
@@ -158,15 +215,13 @@ def _run(dtype, stage, contiguous, windows, dyadic, skip_at=None, inf_at=None, g
     for w in range(windows):
         for m in range(gas):
             skip = (2,) if skip_at == w else ()
-            loss = engine(_coeffs(100 * w + m, dyadic), skip)
+            cs = _coeffs(100 * w + m, dyadic)
+            if inf_at == (w, m):
+                cs[0].view(-1)[0] = float("inf")   # the first parameter's gradient gets an inf
+            loss = engine(cs, skip)
             engine.backward(loss)
             if contiguous:
                 assert all(p.grad is None for p in model.parameters())
-            if inf_at == (w, m):
-                if contiguous:
-                    engine.contiguous.accum[0][10] = float("inf")
-                else:
-                    next(iter(model.parameters())).grad.view(-1)[0] = float("inf")
             applied.append(engine.step())
     return engine, model, applied
 
@@ -203,6 +258,68 @@ def test_flushes_inside_backward_equal_one_flush_at_its_end():
     assert a.grad_norm == b.grad_norm
     assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
     assert torch.equal(a.optimizer.state[0]["exp_avg_sq"], b.optimizer.state[0]["exp_avg_sq"])
+
+
+def _engine(dtype, gas, bucket=None):
+    torch.manual_seed(0)
+    model = Linear({"fp16": torch.float16, "bf16": torch.bfloat16}[dtype]).to(DEV)
+    engine = ms.initialize(model=model, model_parameters=list(model.parameters()),
+                           config=_cfg(dtype, 0, True, gas))
+    if bucket is not None:
+        engine.contiguous.bucket_elements = bucket
+    return engine, model
+
+
+def _windows(engine, gas, windows, start=0, dyadic=False):
+    applied = []
+    for w in range(start, start + windows):
+        for m in range(gas):
+            engine.backward(engine(_coeffs(100 * w + m, dyadic)))
+            applied.append(engine.step())
+    return applied
+
+
+@pytest.mark.parametrize("dtype,bucket", [("fp16", None), ("bf16", None), ("fp16", 1)])
+def test_tile_statistics_give_the_boundary_of_a_scan_of_the_sums(dtype, bucket):
+    """The boundary from K5's tile statistics (folded, no second read of
+    the sums) against the boundary that scans the sums with K1: same
+    decisions and scale, the same fp32 norm (fp64 partial sums in two
+    partitions), the same masters and moments."""
+    a, _ = _engine(dtype, 3, bucket)
+    b, _ = _engine(dtype, 3, bucket)
+    b.contiguous.use_tile_stats = False
+    used = []
+    orig = a.contiguous.tile_stats
+
+    def spy(gi, scale):
+        r = orig(gi, scale)
+        used.append(r is not None)
+        return r
+    a.contiguous.tile_stats = spy
+    for w in range(4):
+        ra, rb = _windows(a, 3, 1, start=w), _windows(b, 3, 1, start=w)
+        assert ra == rb
+        assert a.get_loss_scale() == b.get_loss_scale()
+        assert abs(a.grad_norm - b.grad_norm) <= 1.2e-7 * b.grad_norm, (w, a.grad_norm, b.grad_norm)
+        if a.grad_norm == b.grad_norm:
+            assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
+            assert torch.equal(a.optimizer.state[0]["exp_avg_sq"], b.optimizer.state[0]["exp_avg_sq"])
+    assert used and all(used)
+
+
+def test_a_loss_scale_change_inside_a_window_falls_back_to_scanning_the_sums():
+    a, _ = _engine("fp16", 2)
+    b, _ = _engine("fp16", 2)
+    b.contiguous.use_tile_stats = False
+    scales = iter([a.loss_scaler.loss_scale_factor, 2 * a.loss_scaler.loss_scale_factor])
+    a.contiguous.scale_fn = lambda: next(scales)     # the two flushes unscale differently
+    for m in range(2):
+        a.backward(a(_coeffs(m, False)))
+        b.backward(b(_coeffs(m, False)))
+    assert a.contiguous.tile_stats(0, a.loss_scaler.loss_scale_factor) is None
+    assert a.step() is True and b.step() is True
+    assert a.grad_norm == b.grad_norm
+    assert torch.equal(a.flat_groups[0].data, b.flat_groups[0].data)
 
 
 def test_stage3_equals_stage0():

@@ -66,8 +66,9 @@ int main(void) {
   F(ms_group_scan_t, own_end)
   printf("ms_accum_row_t %zu\n", sizeof(ms_accum_row_t));
   F(ms_accum_row_t, dst) F(ms_accum_row_t, src) F(ms_accum_row_t, numel) F(ms_accum_row_t, first)
-  F(ms_accum_row_t, reserved)
+  F(ms_accum_row_t, reserved) F(ms_accum_row_t, tile_sumsq) F(ms_accum_row_t, tile_flag)
   printf("MS_ACCUM_ROWS_PER_LAUNCH %d\n", MS_ACCUM_ROWS_PER_LAUNCH);
+  printf("MS_ACCUM_TILE %d\n", MS_ACCUM_TILE);
   printf("MS_SCRATCH_MAX_GROUPS %d\n", MS_SCRATCH_MAX_GROUPS);
   printf("MS_ESCRATCH %d\n", MS_ESCRATCH);
   return 0;
@@ -81,6 +82,7 @@ int main(void) {
                "ms_adamw_params_t": _native.AdamWParams, "ms_group_scan_t": _native.GroupScan,
                "ms_accum_row_t": _native.AccumRow}
     assert int(got.pop("MS_ACCUM_ROWS_PER_LAUNCH")) == _native.ACCUM_ROWS_PER_LAUNCH
+    assert int(got.pop("MS_ACCUM_TILE")) == _native.ACCUM_TILE
     assert int(got.pop("MS_SCRATCH_MAX_GROUPS")) == _native.SCRATCH_MAX_GROUPS
     assert int(got.pop("MS_ESCRATCH")) == _native.ESCRATCH
     for key, value in got.items():
@@ -142,15 +144,24 @@ def test_host_argument_errors_return_codes_without_launching():
     # missing address; empty rows launch nothing
     rows = (_native.AccumRow * 3)()
     acc = lib.ms_accumulate_grads
-    assert acc(rows, 3, 5, None) == EINVAL
-    assert acc(rows, -1, 1, None) == EINVAL
-    assert acc(None, 1, 1, None) == EINVAL
-    assert acc(None, 0, 1, None) == 0
-    assert acc(rows, 3, 1, None) == 0                   # three rows of numel 0
-    rows[1] = _native.AccumRow(8, 8, -1, 1, 0)
-    assert acc(rows, 3, 1, None) == EINVAL
-    rows[1] = _native.AccumRow(None, 8, 10, 1, 0)
-    assert acc(rows, 3, 1, None) == EINVAL
+    assert acc(rows, 3, 5, 0, 1.0, None) == EINVAL
+    assert acc(rows, -1, 1, 0, 1.0, None) == EINVAL
+    assert acc(None, 1, 1, 0, 1.0, None) == EINVAL
+    assert acc(None, 0, 1, 0, 1.0, None) == 0
+    assert acc(rows, 3, 1, 0, 1.0, None) == 0           # three rows of numel 0
+    assert acc(rows, 3, 1, _native.SCALE_MULTIPLY, 2.0, None) == EINVAL   # statistics only divide
+    assert acc(rows, 3, 1, _native.SCALE_DIVIDE, 0.0, None) == EINVAL
+    rows[1] = _native.AccumRow(8, 8, -1, 1, 0, None, None)
+    assert acc(rows, 3, 1, 0, 1.0, None) == EINVAL
+    rows[1] = _native.AccumRow(None, 8, 10, 1, 0, None, None)
+    assert acc(rows, 3, 1, 0, 1.0, None) == EINVAL
+    rows[1] = _native.AccumRow(8, 8, 10, 1, 0, 8, None)        # slots come in pairs
+    assert acc(rows, 3, 1, 0, 1.0, None) == EINVAL
+    fold = lib.ms_reduce_tile_stats
+    assert fold(None, None, 0, None, 8, nb, None) == EINVAL
+    assert fold(None, None, 5, 8, 8, nb, None) == EINVAL
+    assert fold(8, 8, -1, 8, 8, nb, None) == EINVAL
+    assert fold(8, 8, 5, 8, 8, nb - 1, None) == EBLOCKS
     assert lib.ms_accumulate_grad(None, None, 1, 0, 1, None) == 0
     assert lib.ms_accumulate_grad(None, 8, 1, 10, 1, None) == EINVAL
     assert lib.ms_accumulate_grad(8, 8, 4, 10, 1, None) == EINVAL
