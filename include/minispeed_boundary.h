@@ -284,9 +284,10 @@ int ms_accumulate_grads(const ms_accum_row_t* rows, int32_t nrows, int32_t src_d
 /*
  * Fold per-tile statistics (K5's tile_sumsq / tile_flag of one group,
  * ntiles slots [dev]) into the nblk >= ms_stats_blocks() partial slots
- * ms_norm_clip reads for that group [dev]: slot j holds the fp64 sum, in
- * slot order, of tiles [j*ntiles/nblk, (j+1)*ntiles/nblk) and the OR of
- * their flags, so the norm is a pure function of the tile statistics.
+ * ms_norm_clip reads for that group [dev]: slot j holds the fp64 sum of
+ * tiles [j*ntiles/nblk, (j+1)*ntiles/nblk) in a fixed order (64 strided
+ * partial sums added by a fixed tree) and the OR of their flags, so the
+ * norm is a pure function of the tile statistics.
  * Replaces K1 (ms_grad_stats) at a contiguous-gradient boundary.
  */
 int ms_reduce_tile_stats(const double* tile_sumsq, const uint32_t* tile_flag, int64_t ntiles,

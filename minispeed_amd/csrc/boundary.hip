@@ -808,26 +808,33 @@ __global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch
 }
 
 // ------------------------------------------------------------------ K2a
-// Thread j folds tiles [j*ntiles/nblk, (j+1)*ntiles/nblk) into partial slot
-// j, in tile order: a fixed partition and order, so the result is a pure
-// function of the tile statistics.
+// One wave per partial slot j: the slot covers tiles [j*ntiles/nblk,
+// (j+1)*ntiles/nblk); lane l adds the tiles lo + l, lo + l + 64, ... in
+// order, and the wave's fixed xor tree adds the lanes.  A fixed partition
+// and order, so the result is a pure function of the tile statistics; the
+// loads of a wave are consecutive slots of memory.
 constexpr int kFoldThreads = 256;
 
 __global__ __launch_bounds__(kFoldThreads) void k_fold_tiles(
     const double* __restrict__ ts, const uint32_t* __restrict__ tf, int64_t ntiles,
     double* __restrict__ bsum, uint32_t* __restrict__ bflag, int nblk) {
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * kFoldThreads + threadIdx.x;
-  if (j >= nblk) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * (kFoldThreads / 64) + (threadIdx.x >> 6);
+  if (j >= nblk) return;   // whole waves
   const int64_t lo = j * ntiles / nblk;
   const int64_t hi = (j + 1) * ntiles / nblk;
   double total = 0.0;
   uint32_t flag = 0;
-  for (int64_t k = lo; k < hi; ++k) {
+  for (int64_t k = lo + lane; k < hi; k += 64) {
     total += ts[k];
     flag |= tf[k];
   }
-  bsum[j] = total;
-  bflag[j] = flag ? 1u : 0u;
+  total = wave_sum(total);
+  const bool bad = __any(flag != 0);
+  if (lane == 0) {
+    bsum[j] = total;
+    bflag[j] = bad ? 1u : 0u;
+  }
 }
 
 // ------------------------------------------------------------- launching
@@ -1205,7 +1212,8 @@ int ms_reduce_tile_stats(const double* tile_sumsq, const uint32_t* tile_flag, in
   if (ntiles > 0 && (!tile_sumsq || !tile_flag)) return MS_EINVAL;
   if (nblk < kStatsBlocks) return MS_EBLOCKS;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((nblk + kFoldThreads - 1) / kFoldThreads);
+  constexpr int kSlotsPerBlock = kFoldThreads / 64;
+  const dim3 grid((nblk + kSlotsPerBlock - 1) / kSlotsPerBlock);
   hipLaunchKernelGGL(k_fold_tiles, grid, dim3(kFoldThreads), 0, st, tile_sumsq, tile_flag,
                      ntiles, block_sumsq, block_flag, nblk);
   return launch_status();

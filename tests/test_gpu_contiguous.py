@@ -132,14 +132,25 @@ def test_batched_accumulation_is_the_fp32_sum_of_every_row(dtype, scale_value):
         assert torch.all(host[~touched] == -3.0), rnd
 
 
+def _wave_fold(x: np.ndarray) -> float:
+    """The fold's order for one slot: lane l adds x[l], x[l + 64], ... in
+    order, then the xor tree (off 32, 16, ..., 1) adds the lanes."""
+    lanes = np.array([np.cumsum(x[lane::64])[-1] if len(x) > lane else 0.0 for lane in range(64)])
+    off = 32
+    while off:
+        lanes = lanes + lanes[np.arange(64) ^ off]
+        off //= 2
+    return float(lanes[0])
+
+
 def test_folding_tile_statistics_sums_fixed_ranges_in_order():
-    """ms_reduce_tile_stats: slot j is the in-order fp64 sum of tiles
+    """ms_reduce_tile_stats: slot j is the fixed-order fp64 sum of tiles
     [j*T/nb, (j+1)*T/nb) and the OR of their flags, every slot written."""
     lib = _native.load()
     nb = _native.stats_blocks()
     stream = _native.stream_handle(torch.device(DEV))
     rng = np.random.default_rng(5)
-    for ntiles in (0, 1, 7, nb - 3, nb, 100_003):
+    for ntiles in (0, 1, 7, nb - 3, nb, 100_003, 3 * nb + 70 * 64 + 5, 130 * nb):
         ts_h = rng.standard_normal(ntiles) ** 2 * 10.0 ** rng.integers(-8, 8, ntiles)
         tf_h = (rng.random(ntiles) < 0.001).astype(np.int32)
         ts = torch.from_numpy(ts_h).to(DEV)
@@ -153,7 +164,7 @@ def test_folding_tile_statistics_sums_fixed_ranges_in_order():
         got_s, got_f = bs.cpu().numpy(), bf.cpu().numpy()
         for j in range(nb):
             lo, hi = j * ntiles // nb, (j + 1) * ntiles // nb
-            want = np.cumsum(ts_h[lo:hi])[-1] if hi > lo else 0.0
+            want = _wave_fold(ts_h[lo:hi])
             assert got_s[j] == want, (ntiles, j)
             assert got_f[j] == (1 if tf_h[lo:hi].any() else 0), (ntiles, j)
 
