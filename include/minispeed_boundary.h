@@ -134,10 +134,13 @@ int ms_abi_version(void);
 const char* ms_error_string(int code);
 
 /* Number of per-group partial slots K1 fills (a constant).  K1 runs
- * min(ms_stats_blocks(), ceil(n / 32768)) blocks over n flat indices, a pure
- * function of n, and zero-fills the remaining slots, so the two-level norm
- * reduction is run-to-run deterministic. */
+ * min(ms_stats_blocks(), ceil(n / ms_stats_min_chunk())) blocks over n flat
+ * indices, a pure function of n, and zero-fills the remaining slots, so the
+ * two-level norm reduction is run-to-run deterministic. */
 int ms_stats_blocks(void);
+
+/* The fewest flat indices K1 gives one block (a constant, 65536). */
+int64_t ms_stats_min_chunk(void);
 
 /*
  * K1 — ragged gradient scan.  Replaces FlatParamGroup.flatten_grads

@@ -131,6 +131,7 @@ SIGNATURES = {
     "ms_abi_version": (ctypes.c_int, []),
     "ms_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ms_stats_blocks": (ctypes.c_int, []),
+    "ms_stats_min_chunk": (ctypes.c_int64, []),
     "ms_grad_stats": (
         ctypes.c_int,
         [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I32, _F, _P, _P, _P, _I32, _P],
@@ -223,6 +224,10 @@ def ms_dtype(dtype: torch.dtype) -> int:
 
 def stats_blocks() -> int:
     return int(load().ms_stats_blocks())
+
+
+def stats_min_chunk() -> int:
+    return int(load().ms_stats_min_chunk())
 
 
 def require_hip_tensor(t: torch.Tensor, what: str) -> None:

@@ -88,7 +88,7 @@ constexpr int kAdamUnroll = MS_ADAM_UNROLL;
 constexpr int kAdamTile = kAdamThreads * kAdamUnroll * 4;          // 512 flat elements (K3)
 constexpr int kStatsBlocks = kStatsBlocksFixed;   // K1 partial slots per group
 #ifndef MS_STATS_MIN_CHUNK
-#define MS_STATS_MIN_CHUNK 32768
+#define MS_STATS_MIN_CHUNK 65536
 #endif
 // K1 gives each block at least this many flat indices: a group of n
 // elements uses min(kStatsBlocks, ceil(n / kStatsMinChunk)) blocks, a pure
@@ -1033,6 +1033,8 @@ const char* ms_error_string(int code) {
 }
 
 int ms_stats_blocks(void) { return kStatsBlocks; }
+
+int64_t ms_stats_min_chunk(void) { return kStatsMinChunk; }
 
 int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
                   int64_t begin, int64_t end, int64_t own_begin,

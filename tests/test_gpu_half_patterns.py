@@ -8,8 +8,9 @@ packed test on 32-bit words (two halves at a time), its scalar path (segment
 edges, misaligned storage) one element at a time; both are run here on all
 65,536 patterns of each half type.
 
-Layout of one launch: n = (16 + #non-finite) x 32768 elements, so K1 runs one
-block per 32768-element range and reports one flag per block.  Blocks 0-15
+Layout of one launch, with B = ms_stats_min_chunk() (65536): n = (16 +
+#non-finite) x B elements, so K1 runs one block per B-element range and
+reports one flag per block.  Blocks 0-15
 hold every finite pattern, eight times over at the eight positions of a
 16-byte vector (block 2s and 2s+1 hold the list rotated by s); block 16+j
 holds non-finite pattern j alone among zeros, at position 8j + (j mod 8) so
@@ -26,11 +27,11 @@ import pytest
 import torch
 
 from oracle import recipe
+from minispeed_amd import _native
 from tests.helpers import DEV, Table, bits, k1, layout_for, store
 
 pytestmark = pytest.mark.gpu
 
-BLOCK = 32768
 FINITE_BLOCKS = 16
 EXP_FIELD = {torch.float16: 0x7C00, torch.bfloat16: 0x7F80}
 
@@ -43,16 +44,17 @@ def _patterns(dtype):
     return finite, nonfinite
 
 
-def _host_buffer(dtype):
+def _host_buffer(dtype, block):
     finite, nonfinite = _patterns(dtype)
     nblk = FINITE_BLOCKS + nonfinite.size
-    buf = np.zeros(nblk * BLOCK, dtype=np.uint16)
-    pair = np.zeros(2 * BLOCK, dtype=np.uint16)
+    assert finite.size <= 2 * block and 8 * nonfinite.size <= block
+    buf = np.zeros(nblk * block, dtype=np.uint16)
+    pair = np.zeros(2 * block, dtype=np.uint16)
     pair[:finite.size] = finite
     for s in range(8):
-        buf[2 * s * BLOCK:(2 * s + 2) * BLOCK] = np.roll(pair, s)
+        buf[2 * s * block:(2 * s + 2) * block] = np.roll(pair, s)
     for j, pat in enumerate(nonfinite):
-        buf[(FINITE_BLOCKS + j) * BLOCK + 8 * j % BLOCK + j % 8] = pat
+        buf[(FINITE_BLOCKS + j) * block + 8 * j + j % 8] = pat
     return buf, nblk
 
 
@@ -60,7 +62,9 @@ def _host_buffer(dtype):
 @pytest.mark.parametrize("aligned", [True, False], ids=["vector", "scalar"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
 def test_every_half_pattern(dtype, aligned, scale):
-    raw, nblk = _host_buffer(dtype)
+    block = _native.stats_min_chunk()
+    raw, nblk = _host_buffer(dtype, block)
+    assert nblk <= _native.stats_blocks()
     n = raw.size
     host = torch.from_numpy(raw.view(np.int16)).view(dtype)
     if aligned:
@@ -83,19 +87,19 @@ def test_every_half_pattern(dtype, aligned, scale):
     np.testing.assert_array_equal(pflag != 0, want_flag)
     assert not psum[nblk:].any()
 
-    fin = FINITE_BLOCKS * BLOCK
+    fin = FINITE_BLOCKS * block
     want = host[:fin].float().div_(scale)
     got = flat[:fin].cpu()
     np.testing.assert_array_equal(bits(got), bits(want))
     for b in range(FINITE_BLOCKS):
-        exact = recipe.sumsq_f64(want[b * BLOCK:(b + 1) * BLOCK].numpy())
+        exact = recipe.sumsq_f64(want[b * block:(b + 1) * block].numpy())
         assert abs(psum[b] - exact) <= 1e-12 * exact, b
 
     # the non-finite blocks: the pattern itself widens to the same inf/nan
-    nf = flat[fin:].cpu().numpy().reshape(-1, BLOCK)
-    src = host[fin:].float().div_(scale).numpy().reshape(-1, BLOCK)
+    nf = flat[fin:].cpu().numpy().reshape(-1, block)
+    src = host[fin:].float().div_(scale).numpy().reshape(-1, block)
     for j in range(nf.shape[0]):
-        k = 8 * j % BLOCK + j % 8
+        k = 8 * j + j % 8
         if np.isnan(src[j, k]):
             assert np.isnan(nf[j, k]), j
         else:
