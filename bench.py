@@ -256,6 +256,9 @@ def bench_llama_shard(args) -> dict:
     nb = _native.stats_blocks()
     psum = torch.empty(nb, dtype=torch.float64, device=dev)
     pflag = torch.empty(nb, dtype=torch.int32, device=dev)
+    ntiles = _native.scan_tiles(hi - lo)
+    tsum = torch.empty(ntiles, dtype=torch.float64, device=dev)
+    tflag = torch.empty(ntiles, dtype=torch.int32, device=dev)
     scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=dev)
     host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
     k2_done = torch.cuda.Event()
@@ -268,8 +271,9 @@ def bench_llama_shard(args) -> dict:
         hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, k + 1)
         tok = t.start("k1") if t else None
         _native.check(lib.ms_grad_stats(tdev.data_ptr(), len(table), _native.DTYPE_BF16, lo, hi,
-                                        lo, hi, 0, 1.0, None, psum.data_ptr(), pflag.data_ptr(),
-                                        nb, stream), "ms_grad_stats")
+                                        lo, hi, 0, 1.0, None, tsum.data_ptr(), tflag.data_ptr(),
+                                        ntiles, psum.data_ptr(), pflag.data_ptr(), nb, stream),
+                      "ms_grad_stats")
         if t:
             t.stop(tok)
         _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 1.0, 0, 1.0,
@@ -412,6 +416,12 @@ def bench_hbm_ceilings(args) -> dict:
         "rmw_1_array": ([at[0]], [at[0]]),
         "rmw_3_arrays": (at[:3], at[:3]),
         "k3_mix": (at[:4], at[:3] + [at[4]]),
+        # K1 writing the fp32 flat gradient and K5's first micro-batch
+        # (read 2, write 4 B/element), K4 (read 4, write 2) and K5's later
+        # micro-batches (read 2 + 4, write 4)
+        "read_1_write_2": ([at[0]], at[1:3]),
+        "read_2_write_1": (at[:2], [at[2]]),
+        "read_3_write_2": (at[:3], at[3:5]),
     }
     out = {}
     for name, (rd, wr) in mixes.items():

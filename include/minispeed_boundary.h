@@ -29,11 +29,17 @@
 extern "C" {
 #endif
 
-#define MS_ABI_VERSION 6
+#define MS_ABI_VERSION 7
 
-/* groups one ms_boundary_scalars_noalloc call can scan (its static scratch:
- * MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() partial slots of 12 bytes) */
+/* groups one ms_boundary_scalars_noalloc call can scan, and the tiles
+ * (MS_SCAN_TILE flat indices each) of the largest one: its static scratch
+ * holds MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() partial slots and
+ * MS_SCRATCH_MAX_TILES tile slots of 12 bytes each (25.5 MiB) */
 #define MS_SCRATCH_MAX_GROUPS 8
+#define MS_SCRATCH_MAX_TILES (1 << 21)
+
+/* flat indices per K1 tile (one wave of 64 lanes scans one tile) */
+#define MS_SCAN_TILE 2048
 
 /* element types of ragged gradient / model storage */
 enum {
@@ -57,8 +63,10 @@ enum {
   MS_OK = 0,
   MS_EINVAL = -1,   /* bad size, range, dtype or NULL where required */
   MS_ETABLE = -2,   /* segment count out of range */
-  MS_EBLOCKS = -3,  /* partial-sum workspace smaller than ms_stats_blocks() */
-  MS_ESCRATCH = -4  /* more groups than MS_SCRATCH_MAX_GROUPS */
+  MS_EBLOCKS = -3,  /* partial-sum workspace smaller than ms_stats_blocks(),
+                       or tile workspace smaller than the scanned range's tiles */
+  MS_ESCRATCH = -4  /* more groups than MS_SCRATCH_MAX_GROUPS, or a group of
+                       more than MS_SCRATCH_MAX_TILES tiles */
 };
 
 /*
@@ -133,14 +141,12 @@ int ms_abi_version(void);
 /* Static text for a return code of this library. */
 const char* ms_error_string(int code);
 
-/* Number of per-group partial slots K1 fills (a constant).  K1 runs
- * min(ms_stats_blocks(), ceil(n / ms_stats_min_chunk())) blocks over n flat
- * indices, a pure function of n, and zero-fills the remaining slots, so the
- * two-level norm reduction is run-to-run deterministic. */
+/* Number of per-group partial slots K2 reduces (a constant, 16384).  K1
+ * writes one statistics slot per tile of MS_SCAN_TILE flat indices and folds
+ * the tiles into these slots in a fixed order (as ms_reduce_tile_stats), so
+ * the norm's reduction order is a pure function of the layout and the norm
+ * is run-to-run deterministic. */
 int ms_stats_blocks(void);
-
-/* The fewest flat indices K1 gives one block (a constant, 65536). */
-int64_t ms_stats_min_chunk(void);
 
 /*
  * K1 — ragged gradient scan.  Replaces FlatParamGroup.flatten_grads
@@ -149,28 +155,36 @@ int64_t ms_stats_min_chunk(void);
  * local_grad_sumsq (flat.py:232-234).
  *
  * Scans flat indices [begin, end) through `segs` [dev] (`nseg` entries,
- * grad dtype `grad_dtype`):
- *   - overflow: block_flag[b] != 0 iff some grad element handled by block b
- *     is inf/nan, tested on the raw stored value (before unscale);
+ * grad dtype `grad_dtype`) in tiles of MS_SCAN_TILE indices, tile t covering
+ * [begin + t*MS_SCAN_TILE, min(begin + (t+1)*MS_SCAN_TILE, end)):
  *   - g = the exact widening fp32(grad), then per `unscale`
  *     (MS_SCALE_*): unchanged, / grad_scale (IEEE division) or
  *     * grad_scale (one rounded multiply);
  *   - flat_grad [dev, optional]: flat_grad[i - begin] = g for every i;
- *   - block_sumsq [dev, optional]: per-block fp64 sum of g*g over the owned
- *     range [own_begin, own_end); with block_flag [dev] it must hold
- *     nblk >= ms_stats_blocks() slots, and all nblk slots are written
- *     (zeros after the last block's).
- * With block_sumsq == NULL and block_flag == NULL the call is a pure ragged
- * flatten (FlatParamGroup.copy_model_to_flat, flat.py:115-131).  flat_grad
- * may be the storage of a single F32 segment spanning [begin, end): each
- * element is read before it is written, by the same lane, so the call then
- * scales the buffer in place (unscale_grads / scale_grads).
+ *   - statistics (block_sumsq != NULL): tile_flag[t] != 0 iff some grad
+ *     element of tile t is inf/nan, tested on the raw stored value (before
+ *     unscale); tile_sumsq[t] = the fp64 sum of g*g over the tile's
+ *     elements inside the owned range [own_begin, own_end), added in a
+ *     fixed order (64 lanes, each its own elements in index order, then a
+ *     fixed tree).  tile_sumsq / tile_flag [dev] need ntiles >=
+ *     ceil((end - begin) / MS_SCAN_TILE) slots (the rest are left alone).
+ *     The tiles are then folded into block_sumsq / block_flag [dev]
+ *     (nblk >= ms_stats_blocks() slots, all written) exactly as
+ *     ms_reduce_tile_stats folds them.
+ * The statistics do not depend on flat_grad: with and without it the slots
+ * get the same bits.  With block_sumsq == NULL (then tile_sumsq, tile_flag
+ * and block_flag must be NULL too) the call is a pure ragged flatten
+ * (FlatParamGroup.copy_model_to_flat, flat.py:115-131).  flat_grad may be the
+ * storage of a single F32 segment spanning [begin, end): each element is
+ * read before it is written, by the same lane, so the call then scales the
+ * buffer in place (unscale_grads / scale_grads).
  */
 int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
                   int64_t begin, int64_t end, int64_t own_begin,
                   int64_t own_end, int32_t unscale, float grad_scale,
-                  float* flat_grad, double* block_sumsq,
-                  uint32_t* block_flag, int32_t nblk, void* stream);
+                  float* flat_grad, double* tile_sumsq, uint32_t* tile_flag,
+                  int64_t ntiles, double* block_sumsq, uint32_t* block_flag,
+                  int32_t nblk, void* stream);
 
 /*
  * K2 — global norm, clip coefficient, skip and loss-scale decision.
@@ -315,15 +329,18 @@ typedef struct ms_group_scan {
  * group (block_sumsq / block_flag of group g at slot g * ms_stats_blocks())
  * followed by ms_norm_clip, bit for bit.
  *
- * groups [host]: ngroups entries, 0 <= ngroups <= MS_SCRATCH_MAX_GROUPS
- *   (more: MS_ESCRATCH, nothing launched).  unscale / grad_scale apply to
- *   every group as in ms_grad_stats; the clip, scaler, out and out_host
- *   arguments are ms_norm_clip's.
- * The partial sums live in a static device array of the library
- * (MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() x 12 bytes = 1.5 MiB), one per
- * GPU, held until the process ends; its address is looked up once per
- * device on the first call there.  K1 writes every slot K2 reads, so nothing
- * must be cleared between calls.  Calls that overlap on one GPU (two streams,
+ * groups [host]: ngroups entries, 0 <= ngroups <= MS_SCRATCH_MAX_GROUPS,
+ *   each of at most MS_SCRATCH_MAX_TILES tiles (ceil((end - begin) /
+ *   MS_SCAN_TILE); more: MS_ESCRATCH, nothing launched).  unscale /
+ *   grad_scale apply to every group as in ms_grad_stats; the clip, scaler,
+ *   out and out_host arguments are ms_norm_clip's.
+ * The tile and partial slots live in a static device array of the library
+ * (MS_SCRATCH_MAX_GROUPS x ms_stats_blocks() + MS_SCRATCH_MAX_TILES slots
+ * of 12 bytes = 25.5 MiB), one per GPU, held until the process ends; its
+ * address is looked up once per device on the first call there.  The groups
+ * are scanned one after another through the same tile slots.  K1 writes
+ * every tile slot the fold reads and the fold every slot K2 reads, so
+ * nothing must be cleared between calls.  Calls that overlap on one GPU (two streams,
  * or two threads) share that array and race: serialize them.
  */
 int ms_boundary_scalars_noalloc(const ms_group_scan_t* groups, int32_t ngroups,

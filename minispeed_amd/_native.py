@@ -19,7 +19,7 @@ from typing import Optional
 import torch  # noqa: F401  (must precede the dlopen below, see module doc)
 
 LIB_NAME = "libminispeed_boundary.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -117,6 +117,8 @@ class AccumRow(ctypes.Structure):
 
 ACCUM_ROWS_PER_LAUNCH = 64
 ACCUM_TILE = 2048
+# flat indices per K1 tile (MS_SCAN_TILE)
+SCAN_TILE = 2048
 
 SEGMENT_BYTES = ctypes.sizeof(Segment)
 SCALARS_BYTES = ctypes.sizeof(StepScalars)
@@ -131,10 +133,9 @@ SIGNATURES = {
     "ms_abi_version": (ctypes.c_int, []),
     "ms_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ms_stats_blocks": (ctypes.c_int, []),
-    "ms_stats_min_chunk": (ctypes.c_int64, []),
     "ms_grad_stats": (
         ctypes.c_int,
-        [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I32, _F, _P, _P, _P, _I32, _P],
+        [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I32, _F, _P, _P, _P, _I64, _P, _P, _I32, _P],
     ),
     "ms_norm_clip": (
         ctypes.c_int,
@@ -157,6 +158,7 @@ SIGNATURES = {
 }
 
 SCRATCH_MAX_GROUPS = 8
+SCRATCH_MAX_TILES = 1 << 21
 ESCRATCH = -4
 
 _lock = threading.Lock()
@@ -226,8 +228,9 @@ def stats_blocks() -> int:
     return int(load().ms_stats_blocks())
 
 
-def stats_min_chunk() -> int:
-    return int(load().ms_stats_min_chunk())
+def scan_tiles(n: int) -> int:
+    """K1's tile slots for a scan of n flat indices."""
+    return (int(n) + SCAN_TILE - 1) // SCAN_TILE
 
 
 def require_hip_tensor(t: torch.Tensor, what: str) -> None:

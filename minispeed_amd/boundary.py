@@ -76,6 +76,12 @@ class Workspace:
         self.partials = torch.empty(n, dtype=torch.float64, device=device)
         self.flags = torch.empty(n, dtype=torch.int32, device=device)
         self.scalars = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=device)
+        # K1's tile slots, shared by the groups of a boundary (each group's
+        # K1 and fold run before the next group's K1, on one stream); grown
+        # on demand, with every stream that used them recorded
+        self.tile_sums: Optional[torch.Tensor] = None
+        self.tile_flags: Optional[torch.Tensor] = None
+        self._tile_streams: set = set()
         # K2 also writes its result here (pinned host memory the device
         # writes directly), so the read-back is a wait on an event recorded
         # after K2: no copy, and K3, queued behind K2, keeps running while
@@ -90,6 +96,22 @@ class Workspace:
             self.partials.data_ptr() + off * 8,
             self.flags.data_ptr() + off * 4,
         )
+
+    def tile_ptrs(self, ntiles: int):
+        """Addresses (sums, flags) of at least ``ntiles`` K1 tile slots for
+        kernels on the current stream."""
+        if self.tile_sums is None or self.tile_sums.numel() < ntiles:
+            # the replaced buffers' memory stays with the streams recorded on
+            # them until those have run what was queued there
+            self.tile_sums = torch.empty(max(1, ntiles), dtype=torch.float64, device=self.device)
+            self.tile_flags = torch.empty(max(1, ntiles), dtype=torch.int32, device=self.device)
+            self._tile_streams = set()
+        cur = torch.cuda.current_stream(self.device)
+        if cur.cuda_stream not in self._tile_streams:
+            self.tile_sums.record_stream(cur)
+            self.tile_flags.record_stream(cur)
+            self._tile_streams.add(cur.cuda_stream)
+        return self.tile_sums.data_ptr(), self.tile_flags.data_ptr()
 
     def read_scalars(self) -> _native.StepScalars:
         """Copy K2's result to pinned memory and wait for the stream."""
@@ -276,12 +298,14 @@ def run_boundary(
             _native.check(rc, "ms_reduce_tile_stats")
         else:
             t1 = g.table("k1").upload(g.boundary_table(0, g.numel_padded, gl.grads, None, gbytes), cur)
+            ntiles = _native.scan_tiles(g.numel_padded)
+            tsum, tflag = ws.tile_ptrs(ntiles)
             tok = timer.start("k1")
             rc = lib.ms_grad_stats(
                 t1[0], t1[1], gdtype, 0, g.numel_padded, lo, hi,
                 _native.SCALE_DIVIDE if unscale else _native.SCALE_NONE, scale32,
                 flat_out.data_ptr() if flat_out is not None else None,
-                psum, pflag, ws.nblk, stream,
+                tsum, tflag, ntiles, psum, pflag, ws.nblk, stream,
             )
             timer.stop(tok)
             _native.check(rc, "ms_grad_stats")
@@ -355,12 +379,14 @@ def scale_in_place(buf: torch.Tensor, mode: int, factor: float) -> None:
     table = _whole_buffer_table(buf)
     _native.check(_native.load().ms_grad_stats(
         table.data_ptr(), 1, _native.DTYPE_F32, 0, n, 0, 0, mode, float(np.float32(factor)),
-        buf.data_ptr(), None, None, 0, _native.stream_handle(buf.device)), "ms_grad_stats(scale)")
+        buf.data_ptr(), None, None, 0, None, None, 0, _native.stream_handle(buf.device)),
+        "ms_grad_stats(scale)")
 
 
 def sumsq_device(buf: torch.Tensor) -> torch.Tensor:
     """``buf.pow(2).sum()`` as a 0-dim fp32 device tensor (flat.py:232-234):
-    K1's fp64 per-block partials summed by K2 and rounded to fp32 once."""
+    K1's fp64 tile partials, folded into K2's slots, summed by K2 and rounded
+    to fp32 once."""
     _native.require_hip_tensor(buf, "sum-of-squares buffer")
     flat = buf.detach().reshape(-1)
     if not flat.is_contiguous():
@@ -373,8 +399,11 @@ def sumsq_device(buf: torch.Tensor) -> torch.Tensor:
     table = _whole_buffer_table(flat)
     stream = _native.stream_handle(flat.device)
     psum, pflag = ws.partial_ptrs(0)
+    ntiles = _native.scan_tiles(n)
+    tsum, tflag = ws.tile_ptrs(ntiles)
     _native.check(lib.ms_grad_stats(table.data_ptr(), 1, _native.ms_dtype(flat.dtype), 0, n, 0, n, 0,
-                                    1.0, None, psum, pflag, ws.nblk, stream), "ms_grad_stats")
+                                    1.0, None, tsum, tflag, ntiles, psum, pflag, ws.nblk, stream),
+                  "ms_grad_stats")
     _native.check(lib.ms_norm_clip(psum, pflag, ws.nblk, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0,
                                    ws.scalars.data_ptr(), None, stream), "ms_norm_clip")
     off = _native.StepScalars.sumsq.offset
@@ -395,8 +424,11 @@ def scan_nonfinite(buf: torch.Tensor) -> bool:
     dev_table = _whole_buffer_table(flat)
     stream = _native.stream_handle(flat.device)
     psum, pflag = ws.partial_ptrs(0)
+    ntiles = _native.scan_tiles(n)
+    tsum, tflag = ws.tile_ptrs(ntiles)
     _native.check(lib.ms_grad_stats(dev_table.data_ptr(), 1, dtype, 0, n, 0, 0, 0, 1.0,
-                                    None, psum, pflag, ws.nblk, stream), "ms_grad_stats")
+                                    None, tsum, tflag, ntiles, psum, pflag, ws.nblk, stream),
+                  "ms_grad_stats")
     _native.check(lib.ms_norm_clip(psum, pflag, ws.nblk, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0,
                                    ws.scalars.data_ptr(), None, stream), "ms_norm_clip")
     return bool(ws.read_scalars().overflow)

@@ -39,22 +39,22 @@
 
 #include "minispeed_boundary.h"
 
-// Partial sums and flags of ms_boundary_scalars_noalloc: for each of
-// MS_SCRATCH_MAX_GROUPS groups kStatsBlocksFixed fp64 sums, then as many
-// uint32 flags.  Host code never names this array directly (its host-side
-// name is not a device address): it uses the per-device address from
-// hipGetSymbolAddress (scratch_base below).
+// Slots of ms_boundary_scalars_noalloc: for each of MS_SCRATCH_MAX_GROUPS
+// groups kStatsBlocksFixed fp64 partial sums, then as many uint32 flags, then
+// MS_SCRATCH_MAX_TILES fp64 tile sums and as many uint32 tile flags (shared
+// by the groups, which are scanned one after another).  Host code never
+// names this array directly (its host-side name is not a device address):
+// it uses the per-device address from hipGetSymbolAddress (scratch_base
+// below).
 #ifndef MS_STATS_BLOCKS
 #define MS_STATS_BLOCKS 16384
 #endif
 constexpr int kStatsBlocksFixed = MS_STATS_BLOCKS;
-static __device__ __align__(256) unsigned char scratch[MS_SCRATCH_MAX_GROUPS * kStatsBlocksFixed *
-                                                       (sizeof(double) + sizeof(uint32_t))];
+static __device__ __align__(256) unsigned char scratch[
+    (static_cast<size_t>(MS_SCRATCH_MAX_GROUPS) * kStatsBlocksFixed + MS_SCRATCH_MAX_TILES) *
+    (sizeof(double) + sizeof(uint32_t))];
 
 namespace {
-
-// K1 block ranges are multiples of kVec elements.
-constexpr int kVec = 8;
 
 // K3, K4 and K5 stream in "wave" order: a tile is T x U quads of 4
 // consecutive elements (T threads, U quads per lane; kStreamThreads x
@@ -86,28 +86,57 @@ constexpr int kStreamTile = kStreamThreads * kStreamUnroll * 4;   // 2048 flat e
 constexpr int kAdamThreads = MS_ADAM_THREADS;
 constexpr int kAdamUnroll = MS_ADAM_UNROLL;
 constexpr int kAdamTile = kAdamThreads * kAdamUnroll * 4;          // 512 flat elements (K3)
-constexpr int kStatsBlocks = kStatsBlocksFixed;   // K1 partial slots per group
-#ifndef MS_STATS_MIN_CHUNK
-#define MS_STATS_MIN_CHUNK 65536
+constexpr int kStatsBlocks = kStatsBlocksFixed;   // K2 partial slots per group
+// K1: one wave scans a run of consecutive tiles of kScanTile flat indices
+// (searching the segment table once and walking on with a cursor), several
+// waves per block, a few 16-byte units of gradient in flight per lane.
+// Which wave scans a tile, and how many units it has in flight, do not
+// change what it computes, so the shape is free per mode.  Over the 1.3B
+// fp16 gradients (292 segments), in isolation: reading only, 8 waves x
+// runs of 4 tiles x 4 units 0.398 ms (runs of 1 / 2 / 8: 0.59 / 0.43 / 0.43;
+// 4 waves: 0.43; 2 units: 0.41); also writing the fp32 flat gradient, one
+// wave x one tile x 2 units 1.370 ms (4 units: 1.40; runs of 2: 1.43).
+constexpr int kScanTile = MS_SCAN_TILE;
+#ifndef MS_SCAN_WAVES_READ
+#define MS_SCAN_WAVES_READ 8
 #endif
-// K1 gives each block at least this many flat indices: a group of n
-// elements uses min(kStatsBlocks, ceil(n / kStatsMinChunk)) blocks, a pure
-// function of n, so the partition (and the norm's bits) never varies run
-// to run, and small groups do not pay for 16384 mostly idle blocks.
-constexpr int64_t kStatsMinChunk = MS_STATS_MIN_CHUNK;
-#ifndef MS_SCAN_THREADS
-#define MS_SCAN_THREADS 512
+#ifndef MS_SCAN_RUN_READ
+#define MS_SCAN_RUN_READ 4
 #endif
-constexpr int kScanThreads = MS_SCAN_THREADS;   // K1 block: 8 wave64
-#ifndef MS_SCAN_DEPTH
-#define MS_SCAN_DEPTH 4
+#ifndef MS_SCAN_DEPTH_READ
+#define MS_SCAN_DEPTH_READ 4
 #endif
-constexpr int kScanDepth = MS_SCAN_DEPTH;   // K1: 16-byte units of gradient in flight per lane
+#ifndef MS_SCAN_WAVES_FLAT
+#define MS_SCAN_WAVES_FLAT 1
+#endif
+#ifndef MS_SCAN_RUN_FLAT
+#define MS_SCAN_RUN_FLAT 1
+#endif
+#ifndef MS_SCAN_DEPTH_FLAT
+#define MS_SCAN_DEPTH_FLAT 2
+#endif
+constexpr int kScanWavesRead = MS_SCAN_WAVES_READ;
+constexpr int kScanWavesFlat = MS_SCAN_WAVES_FLAT;
+// waves per SIMD K1 is compiled for: left alone, the compiler widens every
+// unit of a round before the (serial) fp64 sum and needs 100+ VGPRs (4
+// waves per SIMD); held to 6 it keeps 48-60 (0.398 ms against 0.433 with
+// 5 and 0.428 with 8)
+#ifndef MS_SCAN_MIN_WAVES
+#define MS_SCAN_MIN_WAVES 6
+#endif
 constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
 constexpr int kMaxSegs = 1 << 26;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// Address-space qualifiers for pointers the compiler cannot classify on its
+// own (addresses read from segment tables or kept in structs): global
+// memory and LDS accesses then compile to global_* / ds_* instructions
+// instead of generic flat_* ones, which also count against the
+// scalar-load counter and so lengthen every wait on a scalar load.
+#define MS_GLOBAL __attribute__((address_space(1)))
+#define MS_LDS __attribute__((address_space(3)))
 
 // ---------------------------------------------------------------- dtypes
 // Raw storage <-> fp32.  Widening is exact; narrowing rounds to nearest
@@ -165,7 +194,7 @@ struct DBF16 {
 // aligned, as four 32-bit words, with the non-temporal hint (K1 reads each
 // gradient once).
 __device__ inline void load_unit(const void* p, uint32_t (&w)[4]) {
-  const u4 x = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+  const u4 x = __builtin_nontemporal_load((const MS_GLOBAL u4*)p);
 #pragma unroll
   for (int k = 0; k < 4; ++k) w[k] = x[k];
 }
@@ -229,7 +258,7 @@ __device__ inline bool quad_aligned(const void* p, int64_t elems, int bytes) {
 
 template <class D>
 __device__ inline typename D::raw load_raw1(const void* base, int64_t k) {
-  return reinterpret_cast<const typename D::raw*>(base)[k];
+  return ((const MS_GLOBAL typename D::raw*)base)[k];
 }
 
 template <class D>
@@ -277,163 +306,233 @@ __device__ inline double wave_sum(double x) {
 }
 
 // ------------------------------------------------------------------ K1
-// Block b of the grid (stats_grid(n) blocks) owns the contiguous flat
-// range [begin + b*chunk, begin + (b+1)*chunk), chunk a multiple of kVec,
-// and walks the segments inside it with a cursor.  Each piece of a segment
-// is a scalar head, a vector body of 16-byte units (lane j of the block
-// takes units j, j + kScanThreads, ...) and a scalar tail.  Lanes
-// accumulate their own elements in index order, waves reduce with a fixed
-// xor tree and the wave sums are added in wave order, so the per-block
-// partials and hence the norm are bitwise reproducible run to run.
-template <class G, bool kFlat, bool kStats>
+// One wave scans one tile [r0, r1) of kScanTile flat indices, walking the
+// segments inside it with a cursor.  Each piece of a segment is a scalar
+// head, a vector body of 16-byte units (lane l takes units l, l + 64, ...)
+// and a scalar tail; which path a piece takes depends only on the segment
+// (its gradient's alignment), never on whether the flat gradient is
+// written, so both modes give the same statistics bit for bit.  Lanes
+// accumulate their own elements in index order and the wave reduces with a
+// fixed xor tree, so a tile's partial is a pure function of the layout.
+//
+// Tiles of consecutive waves are adjacent, so the waves resident at any
+// moment read and write one compact window of the flat range; a block per
+// contiguous 1/16384 of the range instead (each resident block streaming
+// its own distant range) wrote the fp32 flat gradient at 4.5 TB/s against
+// 5.8 TB/s this way.
+// K1's scaling of the widened gradient, fixed per launch: none, one rounded
+// multiply by `mul` (the exact reciprocal of a power-of-two loss scale, or
+// scale_grads' factor; unscale1 modes 1 and 3) or IEEE division by `div`
+// (mode 2).  A compile-time choice keeps the per-element path free of
+// branches, so the widened units of a round need not all be held at once.
+enum { kScaleNone = 0, kScaleMul = 1, kScaleDiv = 2 };
+
+template <int kScale>
+__device__ inline float scale_grad(float g, float mul, float div) {
+  if constexpr (kScale == kScaleMul) return g * mul;
+  else if constexpr (kScale == kScaleDiv) return g / div;
+  else return g;
+}
+
+template <class G, bool kFlat, bool kStats, int kScale>
 struct GradScan {
-  int umode;
-  float scale, inv;
+  // 4-byte gradients read at depth 2 (at 4 their read-only scan spills)
+  static constexpr int kScanDepth =
+      kFlat ? MS_SCAN_DEPTH_FLAT : (G::kBytes == 4 ? 2 : MS_SCAN_DEPTH_READ);
+  static constexpr int kUnit = 16 / G::kBytes;   // elements per 16-byte unit
+  // fp16 / bf16 units widen to 32 bytes: staged through LDS so that each
+  // store instruction covers 1 KB of whole lines
+  static constexpr bool kStage = kFlat && kUnit == 8;
+  float mul, div;
   int64_t begin;
-  float* flat;
+  MS_GLOBAL float* flat;
+  MS_LDS f4* slab;       // this wave's 2 KB staging slab (kStage)
   double acc = 0.0;
   bool bad = false;      // per-element inf/nan tests
   uint32_t packed = 0;   // packed exponent tests of the vector body
 
-  __device__ void element(const ms_segment_t& sg, int64_t i, bool count) {
+  template <bool kCount>
+  __device__ void element(const ms_segment_t& sg, int64_t i) {
     float g = 0.0f;
     if (sg.grad) {
       const typename G::raw r = load_raw1<G>(sg.grad, i - sg.begin);
       bad |= G::nonfinite(r);
-      g = unscale1(G::widen(r), umode, scale, inv);
+      g = scale_grad<kScale>(G::widen(r), mul, div);
     }
-    if (kStats && count) {
+    if (kStats && kCount) {
       const double d = static_cast<double>(g);
       acc = __builtin_fma(d, d, acc);
     }
     if (kFlat) flat[i - begin] = g;
   }
 
-  // One unit: the 16 bytes of raw gradient (kUnit consecutive elements,
-  // i .. i + kUnit - 1) a lane moves with one load, as four 32-bit words.
-  static constexpr int kUnit = 16 / G::kBytes;
-  __device__ void unit(const uint32_t (&w)[4], int64_t i, bool count) {
+  // One unit: the 16 bytes of raw gradient a lane moves with one load, as
+  // four 32-bit words, widened (and counted) into g.
+  template <bool kCount>
+  __device__ void widen(const uint32_t (&w)[4], float (&g)[kUnit]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) packed |= (w[j] & G::kExp) + G::kExpOne;
-    float g[kUnit];
 #pragma unroll
     for (int k = 0; k < kUnit; ++k) {
-      g[k] = unscale1(G::widen(unit_elem<G>(w, k)), umode, scale, inv);
-      if (kStats && count) {
+      g[k] = scale_grad<kScale>(G::widen(unit_elem<G>(w, k)), mul, div);
+      if (kStats && kCount) {
         const double d = static_cast<double>(g[k]);
         acc = __builtin_fma(d, d, acc);
       }
     }
-    if (kFlat) {
+  }
+
+  // g -> flat indices i .. i + kUnit - 1; fvec: that range is 16-byte aligned
+  __device__ void put(const float (&g)[kUnit], int64_t i, bool fvec) {
+    MS_GLOBAL float* o = flat + (i - begin);
+    if (fvec) {
 #pragma unroll
       for (int k = 0; k < kUnit; k += 4)
-        *reinterpret_cast<f4*>(flat + (i - begin) + k) = f4{g[k], g[k + 1], g[k + 2], g[k + 3]};
+        __builtin_nontemporal_store(f4{g[k], g[k + 1], g[k + 2], g[k + 3]},
+                                    (MS_GLOBAL f4*)(o + k));
+    } else {
+#pragma unroll
+      for (int k = 0; k < kUnit; ++k) o[k] = g[k];
     }
   }
 
-  // elements [a, b) of segment sg, all inside or all outside the owned range
-  __device__ void piece(const ms_segment_t& sg, int64_t a, int64_t b, bool count, int lane) {
-    const bool vec = sg.grad != nullptr && aligned16(sg.grad) &&
-                     (!kFlat || (aligned16(flat) && ((sg.begin - begin) & (kUnit - 1)) == 0));
+  // The wave's 64 consecutive units, lane l holding unit l, starting at
+  // flat index i0 (16-byte aligned): through the slab, so that each of the
+  // two stores writes 1 KB of whole lines.  Every lane of the wave is active.
+  __device__ void put_wave(const float (&g)[kUnit], int64_t i0, int lane) {
+    slab[2 * lane] = f4{g[0], g[1], g[2], g[3]};
+    slab[2 * lane + 1] = f4{g[4], g[5], g[6], g[7]};
+    __builtin_amdgcn_wave_barrier();
+    const f4 x = slab[lane], y = slab[64 + lane];
+    __builtin_amdgcn_wave_barrier();
+    MS_GLOBAL f4* o = (MS_GLOBAL f4*)(flat + (i0 - begin));
+    __builtin_nontemporal_store(x, o + lane);
+    __builtin_nontemporal_store(y, o + 64 + lane);
+  }
+
+  // elements [a, b) of segment sg, all inside (kCount) or all outside the
+  // owned range
+  template <bool kCount>
+  __device__ void piece(const ms_segment_t& sg, int64_t a, int64_t b, int lane) {
+    const bool vec = sg.grad != nullptr && aligned16(sg.grad);
     if (!vec) {
       if (!sg.grad && !kFlat) return;      // zeros: nothing to count or test
-      for (int64_t i = a + lane; i < b; i += kScanThreads) element(sg, i, count);
+      for (int64_t i = a + lane; i < b; i += 64) element<kCount>(sg, i);
       return;
     }
     const int64_t au = sg.begin + (((a - sg.begin) + kUnit - 1) & ~int64_t(kUnit - 1));
     const int64_t bu = sg.begin + ((b - sg.begin) & ~int64_t(kUnit - 1));
     if (au >= bu) {
-      for (int64_t i = a + lane; i < b; i += kScanThreads) element(sg, i, count);
+      for (int64_t i = a + lane; i < b; i += 64) element<kCount>(sg, i);
       return;
     }
-    for (int64_t i = a + lane; i < au; i += kScanThreads) element(sg, i, count);
-    for (int64_t i = bu + lane; i < b; i += kScanThreads) element(sg, i, count);
+    for (int64_t i = a + lane; i < au; i += 64) element<kCount>(sg, i);
+    for (int64_t i = bu + lane; i < b; i += 64) element<kCount>(sg, i);
     const int64_t nu = (bu - au) / kUnit;
     const char* src = static_cast<const char*>(sg.grad) + (au - sg.begin) * G::kBytes;
-    // Wave order: lane j takes units j, j + kScanThreads, ..., so each load
-    // instruction of a wave reads one contiguous kilobyte of whole cache
+    const bool fvec = kFlat && aligned16((const void*)(flat + (au - begin)));
+    // Wave order: lane l takes units l, l + 64, ..., so each load
+    // instruction of the wave reads one contiguous kilobyte of whole cache
     // lines.  kScanDepth units are in flight per lane; each lane still takes
-    // its units in increasing order, so its running sum (and the block's
-    // partial) does not depend on the depth.
+    // its units in increasing order, so its running sum does not depend on
+    // the depth, on the staging or on the mode.
     int64_t u = lane;
-    for (; u + (kScanDepth - 1) * kScanThreads < nu; u += kScanDepth * kScanThreads) {
-      uint32_t w[kScanDepth][4];
+    if (kStage && fvec) {
+      // rounds in which every lane has all kScanDepth units (a wave-uniform
+      // condition: the slab exchanges data across the wave)
+      for (; (u - lane) + 63 + (kScanDepth - 1) * 64 < nu; u += kScanDepth * 64) {
+        uint32_t w[kScanDepth][4];
 #pragma unroll
-      for (int d = 0; d < kScanDepth; ++d) load_unit(src + (u + d * kScanThreads) * 16, w[d]);
+        for (int d = 0; d < kScanDepth; ++d) load_unit(src + (u + d * 64) * 16, w[d]);
 #pragma unroll
-      for (int d = 0; d < kScanDepth; ++d) unit(w[d], au + (u + d * kScanThreads) * kUnit, count);
+        for (int d = 0; d < kScanDepth; ++d) {
+          float g[kUnit];
+          widen<kCount>(w[d], g);
+          put_wave(g, au + (u - lane + d * 64) * kUnit, lane);
+        }
+      }
+    } else {
+      for (; u + (kScanDepth - 1) * 64 < nu; u += kScanDepth * 64) {
+        uint32_t w[kScanDepth][4];
+#pragma unroll
+        for (int d = 0; d < kScanDepth; ++d) load_unit(src + (u + d * 64) * 16, w[d]);
+#pragma unroll
+        for (int d = 0; d < kScanDepth; ++d) {
+          float g[kUnit];
+          widen<kCount>(w[d], g);
+          if (kFlat) put(g, au + (u + d * 64) * kUnit, fvec);
+        }
+      }
     }
-    for (; u < nu; u += kScanThreads) {
+    for (; u < nu; u += 64) {
       uint32_t w0[4];
       load_unit(src + u * 16, w0);
-      unit(w0, au + u * kUnit, count);
+      float g[kUnit];
+      widen<kCount>(w0, g);
+      if (kFlat) put(g, au + u * kUnit, fvec);
     }
   }
 };
 
-template <class G, bool kFlat, bool kStats>
-__global__ __launch_bounds__(kScanThreads) void k_grad_stats(
+template <bool kFlat>
+constexpr int scan_waves() { return kFlat ? kScanWavesFlat : kScanWavesRead; }
+template <bool kFlat>
+constexpr int scan_run() { return kFlat ? MS_SCAN_RUN_FLAT : MS_SCAN_RUN_READ; }
+
+template <class G, bool kFlat, bool kStats, int kScale>
+__global__ __launch_bounds__(64 * scan_waves<kFlat>(), MS_SCAN_MIN_WAVES) void k_grad_stats(
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
-    int64_t end, int64_t own_begin, int64_t own_end, int umode,
-    float grad_scale, float inv_scale, float* __restrict__ flat,
-    double* __restrict__ bsum, uint32_t* __restrict__ bflag, int nslots) {
-  const int lane = threadIdx.x;
-  GradScan<G, kFlat, kStats> sc;
-  sc.umode = umode;
-  sc.scale = grad_scale;
-  sc.inv = inv_scale;
-  sc.begin = begin;
-  sc.flat = flat;
-  const int64_t n = end - begin;
-  int64_t chunk = (n + gridDim.x - 1) / gridDim.x;
-  chunk = (chunk + kVec - 1) & ~int64_t(kVec - 1);
-  const int64_t r0 = begin + static_cast<int64_t>(blockIdx.x) * chunk;
-  const int64_t r1 = (r0 + chunk < end) ? r0 + chunk : end;
-  if (r0 < r1) {
-    for (int s = find_seg(segs, nseg, r0); s < nseg; ++s) {
-      const ms_segment_t sg = segs[s];
-      const int64_t se = seg_end(sg);
-      const int64_t a = sg.begin > r0 ? sg.begin : r0;
-      const int64_t b = se < r1 ? se : r1;
-      if (a < b) {
-        // split at the owned range so every piece is counted or not
-        const int64_t o0 = own_begin > a ? (own_begin < b ? own_begin : b) : a;
-        const int64_t o1 = own_end < b ? (own_end > o0 ? own_end : o0) : b;
-        if (a < o0) sc.piece(sg, a, o0, false, lane);
-        if (o0 < o1) sc.piece(sg, o0, o1, true, lane);
-        if (o1 < b) sc.piece(sg, o1, b, false, lane);
+    int64_t end, int64_t own_begin, int64_t own_end, float mul, float div,
+    float* __restrict__ flat, double* __restrict__ tsum, uint32_t* __restrict__ tflag,
+    int64_t ntiles) {
+  constexpr int kWaves = scan_waves<kFlat>();
+  constexpr int kRun = scan_run<kFlat>();
+  using Scan = GradScan<G, kFlat, kStats, kScale>;
+  __shared__ f4 slabs[Scan::kStage ? kWaves : 1][128];
+  const int lane = threadIdx.x & 63;
+  // uniform across the wave, and known to be so by the compiler: the tile
+  // bounds, the segment search and the piece bookkeeping stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // a wave's tiles are uniform across it: no block-level barrier anywhere
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves * kRun;
+  for (int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kRun; t0 < ntiles;
+       t0 += stride) {
+    const int64_t t1 = (t0 + kRun < ntiles) ? t0 + kRun : ntiles;
+    // the cursor: the segment holding the next tile's first index
+    int s = find_seg(segs, nseg, begin + t0 * kScanTile);
+    for (int64_t t = t0; t < t1; ++t) {
+      Scan sc;
+      sc.mul = mul;
+      sc.div = div;
+      sc.begin = begin;
+      sc.flat = (MS_GLOBAL float*)flat;
+      sc.slab = (MS_LDS f4*)slabs[Scan::kStage ? wave : 0];
+      const int64_t r0 = begin + t * kScanTile;
+      const int64_t r1 = (r0 + kScanTile < end) ? r0 + kScanTile : end;
+      for (; s < nseg; ++s) {
+        const ms_segment_t sg = segs[s];
+        const int64_t se = seg_end(sg);
+        const int64_t a = sg.begin > r0 ? sg.begin : r0;
+        const int64_t b = se < r1 ? se : r1;
+        if (a < b) {
+          // split at the owned range so every piece is counted or not
+          const int64_t o0 = own_begin > a ? (own_begin < b ? own_begin : b) : a;
+          const int64_t o1 = own_end < b ? (own_end > o0 ? own_end : o0) : b;
+          if (a < o0) sc.template piece<false>(sg, a, o0, lane);
+          if (o0 < o1) sc.template piece<kStats>(sg, o0, o1, lane);
+          if (o1 < b) sc.template piece<false>(sg, o1, b, lane);
+        }
+        if (se > r1) break;   // it also holds the next tile's first index
       }
-      if (se >= r1) break;
-    }
-  }
-  if (kStats) {
-    const bool bad = sc.bad || (sc.packed & G::kTop) != 0;
-    constexpr int kScanWaves = kScanThreads / 64;
-    __shared__ double wsum[kScanWaves];
-    __shared__ uint32_t wbad[kScanWaves];
-    const double w = wave_sum(sc.acc);
-    const bool wb = __any(bad);
-    if ((lane & 63) == 0) {
-      wsum[lane >> 6] = w;
-      wbad[lane >> 6] = wb ? 1u : 0u;
-    }
-    __syncthreads();
-    if (lane == 0) {
-      double total = 0.0;
-      uint32_t flag = 0;
-#pragma unroll
-      for (int k = 0; k < kScanWaves; ++k) {
-        total += wsum[k];
-        flag |= wbad[k];
+      if (kStats) {
+        const bool bad = sc.bad || (sc.packed & G::kTop) != 0;
+        const double w = wave_sum(sc.acc);
+        const bool wb = __any(bad);
+        if (lane == 0) {
+          tsum[t] = w;
+          tflag[t] = wb ? 1u : 0u;
+        }
       }
-      bsum[blockIdx.x] = total;
-      bflag[blockIdx.x] = flag;
-    }
-    // the slots after the last block read as "nothing here" in K2
-    for (int64_t t = static_cast<int64_t>(gridDim.x) + static_cast<int64_t>(blockIdx.x) * kScanThreads + lane;
-         t < nslots; t += static_cast<int64_t>(gridDim.x) * kScanThreads) {
-      bsum[t] = 0.0;
-      bflag[t] = 0u;
     }
   }
 }
@@ -872,38 +971,74 @@ bool valid_dtype(int32_t d) {
   return d == MS_DTYPE_F32 || d == MS_DTYPE_F16 || d == MS_DTYPE_BF16;
 }
 
-// K1's block count for n flat indices (see kStatsMinChunk)
-int stats_grid(int64_t n) {
-  int64_t g = (n + kStatsMinChunk - 1) / kStatsMinChunk;
-  if (g > kStatsBlocks) g = kStatsBlocks;
+// K1's tiles over n flat indices
+int64_t scan_tiles(int64_t n) { return (n + kScanTile - 1) / kScanTile; }
+
+// Grid of K1 (kScanWaves tiles per block); the kernel walks its tiles
+// grid-stride, so a clamped grid still covers every tile.
+int scan_grid(int64_t ntiles, int tiles_per_block) {
+  int64_t g = (ntiles + tiles_per_block - 1) / tiles_per_block;
+  if (g > 0x7fffffff) g = 0x7fffffff;
   if (g < 1) g = 1;
   return static_cast<int>(g);
+}
+
+template <class G, int kScale>
+void launch_stats_s(const ms_segment_t* segs, int nseg, int64_t begin, int64_t end, int64_t ob,
+                    int64_t oe, float mul, float div, float* flat, double* tsum, uint32_t* tflag,
+                    int64_t ntiles, hipStream_t st) {
+  constexpr int kFlatTiles = kScanWavesFlat * MS_SCAN_RUN_FLAT;
+  constexpr int kReadTiles = kScanWavesRead * MS_SCAN_RUN_READ;
+  if (tsum) {
+    if (flat)
+      hipLaunchKernelGGL((k_grad_stats<G, true, true, kScale>), dim3(scan_grid(ntiles, kFlatTiles)),
+                         dim3(64 * kScanWavesFlat), 0, st, segs, nseg, begin, end, ob, oe, mul,
+                         div, flat, tsum, tflag, ntiles);
+    else
+      hipLaunchKernelGGL((k_grad_stats<G, false, true, kScale>), dim3(scan_grid(ntiles, kReadTiles)),
+                         dim3(64 * kScanWavesRead), 0, st, segs, nseg, begin, end, ob, oe, mul,
+                         div, flat, tsum, tflag, ntiles);
+  } else {
+    hipLaunchKernelGGL((k_grad_stats<G, true, false, kScale>), dim3(scan_grid(ntiles, kFlatTiles)),
+                       dim3(64 * kScanWavesFlat), 0, st, segs, nseg, begin, end, ob, oe, mul, div,
+                       flat, tsum, tflag, ntiles);
+  }
 }
 
 template <class G>
 void launch_stats(const ms_segment_t* segs, int nseg, int64_t begin,
                   int64_t end, int64_t ob, int64_t oe, int unscale, float scale,
-                  float* flat, double* bsum, uint32_t* bflag, int nslots,
-                  hipStream_t st) {
-  const bool stats = bsum != nullptr;
+                  float* flat, double* tsum, uint32_t* tflag, hipStream_t st) {
+  const int64_t ntiles = scan_tiles(end - begin);
+  if (ntiles == 0) return;
   float inv = 1.0f;
-  const int umode = unscale_mode(unscale, scale, &inv);
-  const dim3 block(kScanThreads);
-  const dim3 grid(stats_grid(end - begin));
-  if (stats) {
-    if (flat)
-      hipLaunchKernelGGL((k_grad_stats<G, true, true>), grid, block, 0, st, segs,
-                         nseg, begin, end, ob, oe, umode, scale, inv, flat,
-                         bsum, bflag, nslots);
-    else
-      hipLaunchKernelGGL((k_grad_stats<G, false, true>), grid, block, 0, st,
-                         segs, nseg, begin, end, ob, oe, umode, scale, inv,
-                         flat, bsum, bflag, nslots);
-  } else {
-    hipLaunchKernelGGL((k_grad_stats<G, true, false>), grid, block, 0, st, segs,
-                       nseg, begin, end, ob, oe, umode, scale, inv, flat,
-                       bsum, bflag, 0);
+  switch (unscale_mode(unscale, scale, &inv)) {
+    case 0:
+      launch_stats_s<G, kScaleNone>(segs, nseg, begin, end, ob, oe, 1.0f, 1.0f, flat, tsum,
+                                    tflag, ntiles, st);
+      break;
+    case 1:   // x / 2^k as x * 2^-k
+      launch_stats_s<G, kScaleMul>(segs, nseg, begin, end, ob, oe, inv, 1.0f, flat, tsum, tflag,
+                                   ntiles, st);
+      break;
+    case 3:   // x * factor
+      launch_stats_s<G, kScaleMul>(segs, nseg, begin, end, ob, oe, scale, 1.0f, flat, tsum,
+                                   tflag, ntiles, st);
+      break;
+    default:  // x / scale
+      launch_stats_s<G, kScaleDiv>(segs, nseg, begin, end, ob, oe, 1.0f, scale, flat, tsum,
+                                   tflag, ntiles, st);
+      break;
   }
+}
+
+// K2a over ntiles tile slots into nblk partial slots (all written)
+void launch_fold(const double* tsum, const uint32_t* tflag, int64_t ntiles, double* bsum,
+                 uint32_t* bflag, int nblk, hipStream_t st) {
+  constexpr int kSlotsPerBlock = kFoldThreads / 64;
+  const dim3 grid((nblk + kSlotsPerBlock - 1) / kSlotsPerBlock);
+  hipLaunchKernelGGL(k_fold_tiles, grid, dim3(kFoldThreads), 0, st, tsum, tflag, ntiles, bsum,
+                     bflag, nblk);
 }
 
 // Host-side checks of one K1 scan (ms_grad_stats' arguments); MS_OK or the
@@ -919,24 +1054,30 @@ int check_scan(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype, int64
   return MS_OK;
 }
 
-void launch_scan(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype, int64_t begin,
-                 int64_t end, int64_t own_begin, int64_t own_end, int32_t unscale,
-                 float grad_scale, float* flat_grad, double* bsum, uint32_t* bflag,
-                 int32_t nblk, hipStream_t st) {
+// K1 over [begin, end) (tile statistics into tsum / tflag when tsum is not
+// NULL), then, with statistics, K2a folding them into bsum / bflag.
+int launch_scan(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype, int64_t begin,
+                int64_t end, int64_t own_begin, int64_t own_end, int32_t unscale,
+                float grad_scale, float* flat_grad, double* tsum, uint32_t* tflag,
+                double* bsum, uint32_t* bflag, int32_t nblk, hipStream_t st) {
   switch (grad_dtype) {
     case MS_DTYPE_F32:
       launch_stats<DF32>(segs, nseg, begin, end, own_begin, own_end, unscale, grad_scale,
-                         flat_grad, bsum, bflag, nblk, st);
+                         flat_grad, tsum, tflag, st);
       break;
     case MS_DTYPE_F16:
       launch_stats<DF16>(segs, nseg, begin, end, own_begin, own_end, unscale, grad_scale,
-                         flat_grad, bsum, bflag, nblk, st);
+                         flat_grad, tsum, tflag, st);
       break;
     default:
       launch_stats<DBF16>(segs, nseg, begin, end, own_begin, own_end, unscale, grad_scale,
-                          flat_grad, bsum, bflag, nblk, st);
+                          flat_grad, tsum, tflag, st);
       break;
   }
+  int rc = launch_status();
+  if (rc != MS_OK || bsum == nullptr) return rc;
+  launch_fold(tsum, tflag, scan_tiles(end - begin), bsum, bflag, nblk, st);
+  return launch_status();
 }
 
 // Device address of `scratch` on the GPU that `st` belongs to (the current
@@ -1021,10 +1162,11 @@ const char* ms_error_string(int code) {
     case MS_ETABLE:
       return "segment count out of range";
     case MS_EBLOCKS:
-      return "partial-sum workspace smaller than ms_stats_blocks()";
+      return "partial-sum workspace smaller than ms_stats_blocks(), or tile workspace "
+             "smaller than ceil((end - begin) / MS_SCAN_TILE)";
     case MS_ESCRATCH:
-      return "more groups than MS_SCRATCH_MAX_GROUPS (the static scratch of "
-             "ms_boundary_scalars_noalloc)";
+      return "more groups than MS_SCRATCH_MAX_GROUPS, or a group of more than "
+             "MS_SCRATCH_MAX_TILES tiles (the static scratch of ms_boundary_scalars_noalloc)";
     default:
       break;
   }
@@ -1034,23 +1176,25 @@ const char* ms_error_string(int code) {
 
 int ms_stats_blocks(void) { return kStatsBlocks; }
 
-int64_t ms_stats_min_chunk(void) { return kStatsMinChunk; }
-
 int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
                   int64_t begin, int64_t end, int64_t own_begin,
                   int64_t own_end, int32_t unscale, float grad_scale,
-                  float* flat_grad, double* block_sumsq,
-                  uint32_t* block_flag, int32_t nblk, void* stream) {
+                  float* flat_grad, double* tile_sumsq, uint32_t* tile_flag,
+                  int64_t ntiles, double* block_sumsq, uint32_t* block_flag,
+                  int32_t nblk, void* stream) {
   if (!valid_dtype(grad_dtype) || begin < 0 || end < begin) return MS_EINVAL;
-  if ((block_sumsq == nullptr) != (block_flag == nullptr)) return MS_EINVAL;
-  if (block_sumsq == nullptr && flat_grad == nullptr) return MS_EINVAL;
-  if (block_sumsq != nullptr && nblk < kStatsBlocks) return MS_EBLOCKS;
+  const bool stats = block_sumsq != nullptr;
+  if (stats != (block_flag != nullptr) || stats != (tile_sumsq != nullptr) ||
+      stats != (tile_flag != nullptr))
+    return MS_EINVAL;
+  if (!stats && flat_grad == nullptr) return MS_EINVAL;
+  if (stats && (nblk < kStatsBlocks || ntiles < scan_tiles(end - begin))) return MS_EBLOCKS;
   const int rc = check_scan(segs, nseg, grad_dtype, begin, end, unscale, grad_scale);
   if (rc != MS_OK) return rc;
-  if (block_sumsq == nullptr && end == begin) return MS_OK;
-  launch_scan(segs, nseg, grad_dtype, begin, end, own_begin, own_end, unscale, grad_scale,
-              flat_grad, block_sumsq, block_flag, nblk, static_cast<hipStream_t>(stream));
-  return launch_status();
+  if (!stats && end == begin) return MS_OK;
+  return launch_scan(segs, nseg, grad_dtype, begin, end, own_begin, own_end, unscale,
+                     grad_scale, flat_grad, tile_sumsq, tile_flag, block_sumsq, block_flag,
+                     nblk, static_cast<hipStream_t>(stream));
 }
 
 int ms_boundary_scalars_noalloc(const ms_group_scan_t* groups, int32_t ngroups,
@@ -1067,22 +1211,28 @@ int ms_boundary_scalars_noalloc(const ms_group_scan_t* groups, int32_t ngroups,
     const int rc = check_scan(gs.segs, gs.nseg, gs.grad_dtype, gs.begin, gs.end, unscale,
                               grad_scale);
     if (rc != MS_OK) return rc;
+    if (scan_tiles(gs.end - gs.begin) > MS_SCRATCH_MAX_TILES) return MS_ESCRATCH;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   unsigned char* base = nullptr;
   const int rc = scratch_base(st, &base);
   if (rc != MS_OK) return rc;
+  constexpr size_t kSlots = static_cast<size_t>(MS_SCRATCH_MAX_GROUPS) * kStatsBlocks;
   double* sums = reinterpret_cast<double*>(base);
-  uint32_t* flags = reinterpret_cast<uint32_t*>(
-      base + sizeof(double) * MS_SCRATCH_MAX_GROUPS * kStatsBlocks);
+  uint32_t* flags = reinterpret_cast<uint32_t*>(base + sizeof(double) * kSlots);
+  double* tsums = reinterpret_cast<double*>(base + (sizeof(double) + sizeof(uint32_t)) * kSlots);
+  uint32_t* tflags = reinterpret_cast<uint32_t*>(
+      reinterpret_cast<unsigned char*>(tsums) + sizeof(double) * MS_SCRATCH_MAX_TILES);
   for (int g = 0; g < ngroups; ++g) {
     const ms_group_scan_t& gs = groups[g];
-    // every one of the group's kStatsBlocks slots is written (zeros after
-    // the last block), so the array needs no clearing between calls
-    launch_scan(gs.segs, gs.nseg, gs.grad_dtype, gs.begin, gs.end, gs.own_begin, gs.own_end,
-                unscale, grad_scale, nullptr, sums + static_cast<int64_t>(g) * kStatsBlocks,
-                flags + static_cast<int64_t>(g) * kStatsBlocks, kStatsBlocks, st);
-    const int lrc = launch_status();
+    // K1 writes every tile slot of the group and the fold every one of its
+    // kStatsBlocks partial slots, so the array needs no clearing between
+    // calls; the next group's K1 reuses the tile slots after this fold
+    // (same stream)
+    const int lrc = launch_scan(gs.segs, gs.nseg, gs.grad_dtype, gs.begin, gs.end, gs.own_begin,
+                                gs.own_end, unscale, grad_scale, nullptr, tsums, tflags,
+                                sums + static_cast<int64_t>(g) * kStatsBlocks,
+                                flags + static_cast<int64_t>(g) * kStatsBlocks, kStatsBlocks, st);
     if (lrc != MS_OK) return lrc;
   }
   hipLaunchKernelGGL(k_norm_clip, dim3(1), dim3(kNormThreads), 0, st, sums, flags, kStatsBlocks,
@@ -1213,11 +1363,8 @@ int ms_reduce_tile_stats(const double* tile_sumsq, const uint32_t* tile_flag, in
   if (ntiles < 0 || !block_sumsq || !block_flag) return MS_EINVAL;
   if (ntiles > 0 && (!tile_sumsq || !tile_flag)) return MS_EINVAL;
   if (nblk < kStatsBlocks) return MS_EBLOCKS;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  constexpr int kSlotsPerBlock = kFoldThreads / 64;
-  const dim3 grid((nblk + kSlotsPerBlock - 1) / kSlotsPerBlock);
-  hipLaunchKernelGGL(k_fold_tiles, grid, dim3(kFoldThreads), 0, st, tile_sumsq, tile_flag,
-                     ntiles, block_sumsq, block_flag, nblk);
+  launch_fold(tile_sumsq, tile_flag, ntiles, block_sumsq, block_flag, nblk,
+              static_cast<hipStream_t>(stream));
   return launch_status();
 }
 

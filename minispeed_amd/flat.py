@@ -248,9 +248,10 @@ class SegmentTable:
             # and record_stream keeps its memory until that stream is done
             if old.shape[0] == n and old_seen <= {stream.cuda_stream}:
                 dev, seen = old, old_seen
-        if dev is None:
-            dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
-        dev.copy_(staging, non_blocking=True)
+        with torch.cuda.stream(stream):
+            if dev is None:
+                dev = torch.empty((n, 4), dtype=torch.int64, device=self.device)
+            dev.copy_(staging, non_blocking=True)
         if stream.cuda_stream not in seen:
             dev.record_stream(stream)
             seen.add(stream.cuda_stream)
@@ -523,7 +524,7 @@ class FlatParamGroup:
         lib = _native.load()
         rc = lib.ms_grad_stats(
             ptr, n, _native.ms_dtype(dtype), ms, me, ms, me, 0, 1.0,
-            self.data.data_ptr(), None, None, 0, _native.stream_handle(self.device),
+            self.data.data_ptr(), None, None, 0, None, None, 0, _native.stream_handle(self.device),
         )
         _native.check(rc, "ms_grad_stats(flatten)")
         self.masters_written()
@@ -825,7 +826,7 @@ class FlatParamGroup:
         stream = _native.stream_handle(self.device)
         rc = lib.ms_grad_stats(
             ptr, n, _native.ms_dtype(self.model_dtype()), 0, self.numel_padded, 0, 0, 0, 1.0,
-            self.grad.data_ptr(), None, None, 0, stream,
+            self.grad.data_ptr(), None, None, 0, None, None, 0, stream,
         )
         _native.check(rc, "ms_grad_stats(flatten)")
         # gradients of another dtype: their slices hold zeros now; widen them in

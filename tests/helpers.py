@@ -78,20 +78,30 @@ def stream() -> int:
 
 
 def k1(table: Table, dtype: torch.dtype, begin, end, own_begin, own_end, scale=1.0,
-       flat: Optional[torch.Tensor] = None, nblk: Optional[int] = None):
-    """Run ms_grad_stats with stats; return (partials fp64, flags) on CPU."""
+       flat: Optional[torch.Tensor] = None, nblk: Optional[int] = None, tiles: bool = False):
+    """Run ms_grad_stats with stats; return (partials fp64, flags) on CPU,
+    followed with ``tiles`` by (tile sums fp64, tile flags).  The tile slots
+    start as NaN / -1, plus one spare slot that must stay so."""
     lib = _native.load()
     nb = nblk or _native.stats_blocks()
+    nt = _native.scan_tiles(end - begin)
     psum = torch.full((nb,), float("nan"), dtype=torch.float64, device=DEV)
     pflag = torch.full((nb,), -1, dtype=torch.int32, device=DEV)
+    tsum = torch.full((nt + 1,), float("nan"), dtype=torch.float64, device=DEV)
+    tflag = torch.full((nt + 1,), -1, dtype=torch.int32, device=DEV)
     rc = lib.ms_grad_stats(
         table.ptr, table.nseg, _native.ms_dtype(dtype), begin, end, own_begin, own_end,
         1 if scale != 1.0 else 0, float(np.float32(scale)),
-        flat.data_ptr() if flat is not None else None, psum.data_ptr(), pflag.data_ptr(), nb,
-        stream())
+        flat.data_ptr() if flat is not None else None, tsum.data_ptr(), tflag.data_ptr(), nt,
+        psum.data_ptr(), pflag.data_ptr(), nb, stream())
     _native.check(rc, "ms_grad_stats")
     torch.cuda.synchronize()
-    return psum.cpu().numpy(), pflag.cpu().numpy()
+    out = (psum.cpu().numpy(), pflag.cpu().numpy())
+    if tiles:
+        ts, tf = tsum.cpu().numpy(), tflag.cpu().numpy()
+        assert np.isnan(ts[nt]) and tf[nt] == -1, "K1 wrote past its tile slots"
+        out += (ts[:nt], tf[:nt])
+    return out
 
 
 def k2(psum: np.ndarray, pflag: np.ndarray, ngroups=1, has_clip=False, max_norm=0.0,

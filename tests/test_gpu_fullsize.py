@@ -288,10 +288,14 @@ def test_one_rank_shard_step_and_cast_on_gather():
     nb = _native.stats_blocks()
     psum = torch.empty(nb, dtype=torch.float64, device=DEV)
     pflag = torch.empty(nb, dtype=torch.int32, device=DEV)
+    nt = _native.scan_tiles(hi - lo)
+    tsum = torch.empty(nt, dtype=torch.float64, device=DEV)
+    tflag = torch.empty(nt, dtype=torch.int32, device=DEV)
     scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
     st = _native.stream_handle(torch.device(DEV))
     _native.check(lib.ms_grad_stats(tdev.data_ptr(), len(table), _native.DTYPE_BF16, lo, hi, lo, hi,
-                                    0, 1.0, None, psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
+                                    0, 1.0, None, tsum.data_ptr(), tflag.data_ptr(), nt,
+                                    psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
     _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 0.05, 0, 1.0, 0, 0,
                                    1000, 1.0, 2.0 ** 24, scal.data_ptr(), None, st), "k2")
     hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 4)
@@ -446,10 +450,14 @@ def test_llama3_8b_rank3_of_8_shard_at_its_exact_geometry():
     nb = _native.stats_blocks()
     psum = torch.empty(nb, dtype=torch.float64, device=DEV)
     pflag = torch.empty(nb, dtype=torch.int32, device=DEV)
+    nt = _native.scan_tiles(hi - lo)
+    tsum = torch.empty(nt, dtype=torch.float64, device=DEV)
+    tflag = torch.empty(nt, dtype=torch.int32, device=DEV)
     scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
     st = _native.stream_handle(torch.device(DEV))
     _native.check(lib.ms_grad_stats(tdev.data_ptr(), pieces, _native.DTYPE_BF16, lo, hi, lo, hi,
-                                    0, 1.0, None, psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
+                                    0, 1.0, None, tsum.data_ptr(), tflag.data_ptr(), nt,
+                                    psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
     _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 1.0, 0, 1.0, 0, 0,
                                    1000, 1.0, 2.0 ** 24, scal.data_ptr(), None, st), "k2")
     hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, 3)

@@ -331,6 +331,9 @@ def test_boundary_kernels_replay_in_a_hip_graph():
     nb = _native.stats_blocks()
     psum = torch.empty(nb, dtype=torch.float64, device=DEV)
     pflag = torch.empty(nb, dtype=torch.int32, device=DEV)
+    nt = _native.scan_tiles(n)
+    tsum = torch.empty(nt, dtype=torch.float64, device=DEV)
+    tflag = torch.empty(nt, dtype=torch.int32, device=DEV)
     scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
     gen = torch.Generator(device=DEV).manual_seed(3)
     p0 = torch.randn(n, generator=gen, device=DEV) * 0.02
@@ -341,7 +344,8 @@ def test_boundary_kernels_replay_in_a_hip_graph():
 
     def boundary(st):
         _native.check(lib.ms_grad_stats(table.ptr, table.nseg, _native.DTYPE_F16, 0, n, 0, n, 1,
-                                        1024.0, None, psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
+                                        1024.0, None, tsum.data_ptr(), tflag.data_ptr(), nt,
+                                        psum.data_ptr(), pflag.data_ptr(), nb, st), "k1")
         _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 0.5, 1, 1024.0,
                                        3, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), None, st), "k2")
         _native.check(lib.ms_fused_adamw(p.data_ptr(), m.data_ptr(), v.data_ptr(), None, table.ptr,

@@ -70,6 +70,8 @@ int main(void) {
   printf("MS_ACCUM_ROWS_PER_LAUNCH %d\n", MS_ACCUM_ROWS_PER_LAUNCH);
   printf("MS_ACCUM_TILE %d\n", MS_ACCUM_TILE);
   printf("MS_SCRATCH_MAX_GROUPS %d\n", MS_SCRATCH_MAX_GROUPS);
+  printf("MS_SCRATCH_MAX_TILES %d\n", MS_SCRATCH_MAX_TILES);
+  printf("MS_SCAN_TILE %d\n", MS_SCAN_TILE);
   printf("MS_ESCRATCH %d\n", MS_ESCRATCH);
   return 0;
 }
@@ -84,6 +86,8 @@ int main(void) {
     assert int(got.pop("MS_ACCUM_ROWS_PER_LAUNCH")) == _native.ACCUM_ROWS_PER_LAUNCH
     assert int(got.pop("MS_ACCUM_TILE")) == _native.ACCUM_TILE
     assert int(got.pop("MS_SCRATCH_MAX_GROUPS")) == _native.SCRATCH_MAX_GROUPS
+    assert int(got.pop("MS_SCRATCH_MAX_TILES")) == _native.SCRATCH_MAX_TILES
+    assert int(got.pop("MS_SCAN_TILE")) == _native.SCAN_TILE
     assert int(got.pop("MS_ESCRATCH")) == _native.ESCRATCH
     for key, value in got.items():
         if "." in key:
@@ -97,13 +101,25 @@ def test_host_argument_errors_return_codes_without_launching():
     lib = _native.load()
     EINVAL, ETABLE, EBLOCKS = -1, -2, -3
     nb = _native.stats_blocks()
-    # bad dtype / negative range / missing outputs / small workspace / empty table
-    assert lib.ms_grad_stats(None, 0, 7, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb, None) == EINVAL
-    assert lib.ms_grad_stats(None, 0, 1, 10, 5, 0, 10, 0, 1.0, None, 8, 8, nb, None) == EINVAL
-    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, None, None, nb, None) == EINVAL
-    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb - 1, None) == EBLOCKS
-    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 0, 1.0, None, 8, 8, nb, None) == ETABLE
-    assert lib.ms_grad_stats(None, 0, 1, 0, 10, 0, 10, 1, 0.0, 8, None, None, nb, None) == ETABLE
+    tile = _native.SCAN_TILE
+
+    def k1(segs, nseg, dtype, begin, end, unscale, scale, flat, ts, tf, nt, bs, bf, nblk):
+        return lib.ms_grad_stats(segs, nseg, dtype, begin, end, begin, end, unscale, scale, flat,
+                                 ts, tf, nt, bs, bf, nblk, None)
+    # bad dtype / negative range / missing outputs / unpaired statistics
+    # pointers / small workspaces / empty table
+    assert k1(None, 0, 7, 0, 10, 0, 1.0, None, 8, 8, 1, 8, 8, nb) == EINVAL
+    assert k1(None, 0, 1, 10, 5, 0, 1.0, None, 8, 8, 1, 8, 8, nb) == EINVAL
+    assert k1(None, 0, 1, 0, 10, 0, 1.0, None, None, None, 1, None, None, nb) == EINVAL
+    assert k1(None, 0, 1, 0, 10, 0, 1.0, None, None, None, 1, 8, 8, nb) == EINVAL
+    assert k1(None, 0, 1, 0, 10, 0, 1.0, None, 8, None, 1, 8, 8, nb) == EINVAL
+    assert k1(None, 0, 1, 0, 10, 0, 1.0, None, 8, 8, 1, None, None, nb) == EINVAL
+    assert k1(None, 0, 1, 0, 10, 0, 1.0, None, 8, 8, 1, 8, 8, nb - 1) == EBLOCKS
+    assert k1(None, 0, 1, 0, 10, 0, 1.0, None, 8, 8, 0, 8, 8, nb) == EBLOCKS
+    assert k1(None, 0, 1, 0, 2 * tile + 1, 0, 1.0, None, 8, 8, 2, 8, 8, nb) == EBLOCKS
+    assert k1(None, 0, 1, 0, 2 * tile + 1, 0, 1.0, None, 8, 8, 3, 8, 8, nb) == ETABLE
+    assert k1(None, 0, 1, 0, 10, 0, 1.0, None, 8, 8, 1, 8, 8, nb) == ETABLE
+    assert k1(None, 0, 1, 0, 10, 1, 0.0, 8, None, None, 0, None, None, nb) == ETABLE
     assert lib.ms_norm_clip(None, None, nb, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, None, None,
                             None) == EINVAL
     assert lib.ms_norm_clip(8, 8, nb - 1, 1, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None,
@@ -121,9 +137,8 @@ def test_host_argument_errors_return_codes_without_launching():
     hp.grad_scale = 2.0
     assert lib.ms_fused_adamw(8, 8, 8, None, 8, 1, 1, 1, 0, 10, ctypes.byref(hp), 8, None) == EINVAL
     # K1: scaling mode out of range; divide by a non-positive scale
-    assert lib.ms_grad_stats(8, 1, 0, 0, 10, 0, 0, 3, 1.0, 8, None, None, 0, None) == EINVAL
-    assert lib.ms_grad_stats(8, 1, 0, 0, 10, 0, 0, _native.SCALE_DIVIDE, -1.0, 8, None, None, 0,
-                             None) == EINVAL
+    assert k1(8, 1, 0, 0, 10, 3, 1.0, 8, None, None, 0, None, None, 0) == EINVAL
+    assert k1(8, 1, 0, 0, 10, _native.SCALE_DIVIDE, -1.0, 8, None, None, 0, None, None, 0) == EINVAL
     assert lib.ms_cast_to_model(None, 0, 10, 8, 1, 1, None) == EINVAL
     assert lib.ms_cast_to_model(8, 0, 10, None, 0, 1, None) == ETABLE
     assert lib.ms_cast_to_model(8, 0, 10, 8, 1, 5, None) == EINVAL
@@ -140,6 +155,10 @@ def test_host_argument_errors_return_codes_without_launching():
     assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == EINVAL
     scans[0] = _native.GroupScan(None, 0, 1, 0, 10, 0, 10)
     assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == ETABLE
+    # a group with more tiles than the scratch holds
+    big = _native.SCRATCH_MAX_TILES * _native.SCAN_TILE + 1
+    scans[0] = _native.GroupScan(8, 1, 1, 0, big, 0, big)
+    assert noalloc(scans, 1, 0, 1.0, 0, 0.0, 0, 1.0, 0, 0, 1, 1.0, 1.0, 8, None, None) == _native.ESCRATCH
     # batched K5: dtype, row count, a NULL row array, a negative size, a
     # missing address; empty rows launch nothing
     rows = (_native.AccumRow * 3)()

@@ -1,7 +1,7 @@
 """ms_boundary_scalars_noalloc against the entry points it stands for.
 
-The no-allocation entry point runs K1 over every group with its partial sums
-in the library's static scratch array, then K2.  Its result must equal, bit
+The no-allocation entry point runs K1 and the fold over every group with its
+tile and partial slots in the library's static scratch array, then K2.  Its result must equal, bit
 for bit, ms_grad_stats per group into a caller workspace followed by
 ms_norm_clip, on two calls in a row, the second with a smaller input (the
 scratch keeps the first call's contents).  Groups are ragged fp16 / bf16 /
@@ -54,8 +54,12 @@ def _with_workspace(lib, scans, stream, **kw):
     psum = torch.empty(len(scans) * nb, dtype=torch.float64, device=DEV)
     pflag = torch.empty(len(scans) * nb, dtype=torch.int32, device=DEV)
     for g, s in enumerate(scans):
+        nt = _native.scan_tiles(s.end - s.begin)
+        tsum = torch.empty(max(1, nt), dtype=torch.float64, device=DEV)
+        tflag = torch.empty(max(1, nt), dtype=torch.int32, device=DEV)
         _native.check(lib.ms_grad_stats(s.segs, s.nseg, s.grad_dtype, s.begin, s.end, s.own_begin,
                                         s.own_end, kw["unscale"], kw["grad_scale"], None,
+                                        tsum.data_ptr(), tflag.data_ptr(), nt,
                                         psum.data_ptr() + 8 * g * nb, pflag.data_ptr() + 4 * g * nb,
                                         nb, stream), "ms_grad_stats")
     out = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
