@@ -104,6 +104,45 @@ def test_k1_partials_are_deterministic():
     np.testing.assert_array_equal(a.view(np.int64), b.view(np.int64))
 
 
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+@pytest.mark.parametrize("layout", ["ragged", "aligned", "misaligned", "shard"])
+def test_k1_tile_statistics_do_not_depend_on_the_flat_output(dtype, layout):
+    """Writing the flat gradient changes no statistics bit (the piece paths
+    depend on the gradient storage alone), and tile t's fp64 sum is the
+    exact sum of squares of its owned elements [t*2048, (t+1)*2048) to
+    1e-12: the tile boundaries sit where the header says."""
+    shapes = ALIGNED + RAGGED if layout != "aligned" else ALIGNED
+    grads = ragged_grads(shapes, dtype, 1e-3, seed=41)
+    dg = _device(grads)
+    if layout == "misaligned":
+        # 2-byte (fp16/bf16) or 4-byte (fp32) aligned storage: per-element path
+        for k in (0, 3):
+            base = torch.zeros(dg[k].numel() + 1, dtype=dtype, device=DEV)
+            base[1:].copy_(dg[k].reshape(-1))
+            dg[k] = base[1:].view(dg[k].shape)
+            assert dg[k].data_ptr() % 16 != 0
+    world, rank, stage = (3, 1, 2) if layout == "shard" else (1, 0, 0)
+    lay, tab = _grad_table(shapes, dg, world, rank, stage)
+    n = lay.numel_padded
+    lo, hi = (lay.shard_start, lay.shard_end) if layout == "shard" else (0, n)
+    flat = torch.full((n,), float("nan"), device=DEV)
+    with_flat = k1(tab, dtype, 0, n, lo, hi, flat=flat, tiles=True)
+    without = k1(tab, dtype, 0, n, lo, hi, tiles=True)
+    for a, b in zip(with_flat, without):
+        np.testing.assert_array_equal(a.view(np.uint8), b.view(np.uint8))
+    psum, pflag, tsum, tflag = without
+    assert tsum.size == -(-n // _native.SCAN_TILE) and not tflag.any()
+    want, _ = _oracle_flat(shapes, grads, 1.0)
+    np.testing.assert_array_equal(bits(flat), bits(want))
+    owned = want.numpy().copy()
+    owned[:lo] = 0.0
+    owned[hi:] = 0.0
+    T = _native.SCAN_TILE
+    for t in range(tsum.size):
+        exact = recipe.sumsq_f64(owned[t * T:(t + 1) * T])
+        assert abs(tsum[t] - exact) <= 1e-12 * exact, t
+
+
 def test_k1_owned_range_only_counts_owned_elements():
     shapes = RAGGED
     grads = ragged_grads(shapes, F32, 1e-2, seed=5)
