@@ -320,6 +320,7 @@ __device__ inline double wave_sum(double x) {
 // contiguous 1/16384 of the range instead (each resident block streaming
 // its own distant range) wrote the fp32 flat gradient at 4.5 TB/s against
 // 5.8 TB/s this way.
+
 // K1's scaling of the widened gradient, fixed per launch: none, one rounded
 // multiply by `mul` (the exact reciprocal of a power-of-two loss scale, or
 // scale_grads' factor; unscale1 modes 1 and 3) or IEEE division by `div`
