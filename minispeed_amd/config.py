@@ -206,12 +206,12 @@ class DeepSpeedConfig:
 
         return getattr(torch, _TORCH_DTYPE_NAMES[self.dtype])
 
-    def __repr__(self) -> str:  # pragma: no cover - debug helper
-        return (
-            f"DeepSpeedConfig(dtype={self.dtype}, zero_stage={self.zero_stage}, "
-            f"micro_batch={self.micro_batch}, gas={self.gas}, "
-            f"world_size={self.world_size}, clip={self.gradient_clipping})"
-        )
+    _SHOWN = ("dtype", "zero_stage", "gas", "micro_batch", "gradient_clipping",
+              "state_spacing_bytes", "materialize_flat_grad", "contiguous_gradients")
+
+    def __repr__(self) -> str:
+        shown = ", ".join(f"{k}={getattr(self, k, None)!r}" for k in self._SHOWN)
+        return f"{type(self).__name__}({shown})"
 
 
 def load_config(
