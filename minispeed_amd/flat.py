@@ -496,10 +496,6 @@ class FlatParamGroup:
             t = self._tables[key] = SegmentTable(self.device)
         return t
 
-    def _storage(self, t: torch.Tensor, rng: Range):
-        _native.require_hip_tensor(t, "parameter storage")
-        return (t.data_ptr(), rng, t.element_size())
-
     def model_storages(self) -> List[Optional[tuple]]:
         out = []
         for (offset, p), n in zip(self._offsets, self._numels):
@@ -511,15 +507,31 @@ class FlatParamGroup:
         return out
 
     # -------------------------------------------------------- conversions
+    def _model_table(self, lo: int, hi: int, as_source: bool) -> np.ndarray:
+        """Segment table of ``[lo, hi)`` over the parameters' storage, in
+        the gradient column (the source K1 widens) or in the model column
+        (the target K4 narrows into).  The whole padded range of full-size
+        parameters takes the cached rows and the C++ pointer walk; anything
+        else (a shard, ZeRO-3 placeholders) the general table."""
+        if (lo, hi) == (0, self.numel_padded) and not self._partitioned:
+            ptrs = self.model_pointers()
+            if as_source:
+                return self.boundary_table(lo, hi, ptrs, None, _ELEM_BYTES[self.model_dtype()])
+            return self.boundary_table(lo, hi, None, ptrs)
+        stores = self.model_storages()
+        none = [None] * len(stores)
+        table = (self.layout.segments(lo, hi, stores, none) if as_source
+                 else self.layout.segments(lo, hi, none, stores))
+        check_table(table, lo, hi)
+        return table
+
     @torch.no_grad()
     def copy_model_to_flat(self) -> None:
         """Snapshot the parameters covered by ``master_range`` into ``data``
         (flat.py:115-131): a ragged widening copy on the GPU."""
         ms, me = self.master_range
         dtype = self.model_dtype()
-        stores = self.model_storages()
-        table = self.layout.segments(ms, me, stores, [None] * len(stores))
-        check_table(table, ms, me)
+        table = self._model_table(ms, me, as_source=True)
         ptr, n = self.table("to_flat").upload(table)
         lib = _native.load()
         rc = lib.ms_grad_stats(
@@ -545,10 +557,9 @@ class FlatParamGroup:
         if into_shard and (base, end) == (self.shard_start, self.shard_end):
             # the parameters tile model_shard: one contiguous segment
             table = np.array([[base, end - base, 0, self.model_shard.data_ptr()]], dtype=np.int64)
+            check_table(table, base, end)
         else:
-            stores = self.model_storages()
-            table = self.layout.segments(base, end, [None] * len(stores), stores)
-        check_table(table, base, end)
+            table = self._model_table(base, end, as_source=False)
         ptr, n = self.table("to_model").upload(table)
         rc = _native.load().ms_cast_to_model(
             buf.data_ptr(), base, end, ptr, n, _native.ms_dtype(dtype),
@@ -780,33 +791,6 @@ class FlatParamGroup:
         return table
 
     # ----------------------------------------------------------- grads
-    def grad_storages(self) -> Tuple[List[Optional[tuple]], List[torch.Tensor], List[tuple]]:
-        """Ragged gradient storage of every parameter, in group order.
-
-        Returns the storage descriptors of the gradients in the group's
-        dtype (``None`` for the others), the tensors they point into (the
-        caller keeps those alive until the kernels reading them have run),
-        and ``(flat offset, numel, tensor)`` of every gradient in another
-        floating dtype.
-        """
-        stores: List[Optional[tuple]] = []
-        keep: List[torch.Tensor] = []
-        foreign: List[tuple] = []
-        dtype = self.model_dtype()
-        for (offset, p), n in zip(self._offsets, self._numels):
-            g = p.grad
-            if g is None:
-                stores.append(None)
-                continue
-            g = self._check_grad(g.detach(), n)
-            keep.append(g)
-            if g.dtype == dtype:
-                stores.append(self._storage(g, (offset, offset + n)))
-            else:
-                stores.append(None)
-                foreign.append((offset, n, g))
-        return stores, keep, foreign
-
     def release_grads(self) -> None:
         for p in self.params:
             p.grad = None
@@ -818,22 +802,19 @@ class FlatParamGroup:
         exactly, ``param.grad`` is released."""
         if self.grad is None:
             self.grad = torch.empty(self.numel_padded, dtype=torch.float32, device=self.device)
-        stores, keep, foreign = self.grad_storages()
-        table = self.layout.segments(0, self.numel_padded, stores, [None] * len(stores))
-        check_table(table, 0, self.numel_padded)
+        # the C++ walk of the gradients; a gradient in another floating dtype
+        # makes every address point into one exactly widened fp32 buffer
+        ptrs, keep, gdtype = self.grad_pointers()
+        if gdtype is None:
+            gdtype = _native.ms_dtype(self.model_dtype())
+        gbytes = 4 if gdtype == _native.DTYPE_F32 else 2
+        table = self.boundary_table(0, self.numel_padded, ptrs, None, gbytes)
         ptr, n = self.table("flatten").upload(table)
-        lib = _native.load()
-        stream = _native.stream_handle(self.device)
-        rc = lib.ms_grad_stats(
-            ptr, n, _native.ms_dtype(self.model_dtype()), 0, self.numel_padded, 0, 0, 0, 1.0,
-            self.grad.data_ptr(), None, None, 0, None, None, 0, stream,
+        rc = _native.load().ms_grad_stats(
+            ptr, n, gdtype, 0, self.numel_padded, 0, 0, 0, 1.0, self.grad.data_ptr(),
+            None, None, 0, None, None, 0, _native.stream_handle(self.device),
         )
         _native.check(rc, "ms_grad_stats(flatten)")
-        # gradients of another dtype: their slices hold zeros now; widen them in
-        for off, numel, g in foreign:
-            _native.check(lib.ms_accumulate_grad(self.grad.data_ptr() + 4 * off, g.data_ptr(),
-                                                 _native.ms_dtype(g.dtype), numel, 1, stream),
-                          "ms_accumulate_grad(widen)")
         self._grad_dirty = True
         self.release_grads()
         # the gradients may have been allocated on another stream: their
