@@ -89,6 +89,9 @@ def parse(argv=None):
     ap.add_argument("--workload", default="gpt-1.3b")
     ap.add_argument("--grad-dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
     ap.add_argument("--mode", default="fused", choices=["fused", "materialize", "contiguous"])
+    ap.add_argument("--micro-batches", type=int, default=1,
+                    help="with --mode contiguous: gradient accumulation steps per window (the "
+                         "hooks add each micro-batch's gradients into the fp32 sums)")
     ap.add_argument("--zero-stage", type=int, default=1, choices=[0, 1, 2, 3],
                     help="ZeRO stage at world size 1 (3: also times the parameter gather)")
     ap.add_argument("--state-spacing-gib", type=_spacing, default="auto",
@@ -108,10 +111,11 @@ def parse(argv=None):
     return ap.parse_args(argv)
 
 
-def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1, state_spacing_gib="auto") -> dict:
+def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1, state_spacing_gib="auto",
+                  gas: int = 1) -> dict:
     cfg = {
         "train_micro_batch_size_per_gpu": 1,
-        "gradient_accumulation_steps": 1,
+        "gradient_accumulation_steps": gas,
         "gradient_clipping": 1.0,
         "dtype": grad_dtype,
         "optimizer": {"type": "AdamW",
@@ -474,6 +478,11 @@ def main(argv=None) -> int:
         print(json.dumps({"error": f"--gpus {args.gpus}: bench.py measures the boundary step on one "
                                    "GPU; multi-GPU runs are not part of it"}))
         return 2
+    if args.micro_batches < 1 or (args.micro_batches > 1 and args.mode != "contiguous"):
+        print(json.dumps({"error": "--micro-batches > 1 applies to --mode contiguous only: in the "
+                                   "other modes micro-batches accumulate in autograd, outside "
+                                   "the boundary step"}))
+        return 2
     import numpy as np
     import torch
     from torch import nn
@@ -512,7 +521,8 @@ def main(argv=None) -> int:
         params = [nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
         module = nn.ParameterList(params)
         engine = ms.initialize(model=module, model_parameters=list(module),
-                               config=engine_config(args.grad_dtype, args.mode, args.zero_stage, spacing))
+                               config=engine_config(args.grad_dtype, args.mode, args.zero_stage, spacing,
+                                                    args.micro_batches))
         while len(grad_sets) < 2:
             grad_sets.append([(torch.randn(*s, generator=gen, device=dev) * (1e-3 * mult)).to(gdt)
                               for s in shapes])
@@ -522,7 +532,7 @@ def main(argv=None) -> int:
         window = (st0["exp_avg"].data_ptr() - g0.data.data_ptr()) / 2 ** 30 if same else 0.0
         torch.cuda.synchronize()
         log(f"[bench] state placement {spacing!r}: window {window:g} GiB; warming up")
-        gather_s, accum_s = [], []
+        gather_s, accum_s = [], []   # accum_s: (micro-batch index, seconds)
 
         def attach(k: int, measure: bool = False) -> None:
             """What the last backward of a window leaves: grads on every param
@@ -538,9 +548,14 @@ def main(argv=None) -> int:
                 if measure:
                     torch.cuda.synchronize()
                     gather_s.append(time.perf_counter() - t0)
-            for p, g in zip(params, grad_sets[k % 2]):
-                p.grad = g
-            if engine.contiguous is not None:
+            if engine.contiguous is None:
+                for p, g in zip(params, grad_sets[k % 2]):
+                    p.grad = g
+                engine.micro_steps += 1
+                return
+            for m in range(args.micro_batches):
+                for p, g in zip(params, grad_sets[(k + m) % 2]):
+                    p.grad = g
                 if measure:
                     torch.cuda.synchronize()
                     t0 = time.perf_counter()
@@ -549,8 +564,8 @@ def main(argv=None) -> int:
                 engine.contiguous.flush()
                 if measure:
                     torch.cuda.synchronize()
-                    accum_s.append(time.perf_counter() - t0)
-            engine.micro_steps += 1
+                    accum_s.append((m, time.perf_counter() - t0))
+                engine.micro_steps += 1
 
         def boundary() -> None:
             if not engine.step():
@@ -606,7 +621,10 @@ def main(argv=None) -> int:
                "k_ms": ({k: float(np.mean(timer.durations_ms(k))) for k in ("k1", "k2", "k3")}
                         if kernel_timing else None)}
         if accum_s:
-            out["accumulate_ms"] = float(np.mean(accum_s)) * 1e3
+            first = [t for m, t in accum_s if m == 0]
+            later = [t for m, t in accum_s if m > 0]
+            out["accumulate_ms"] = {"first": float(np.mean(first)) * 1e3,
+                                    "later": float(np.mean(later)) * 1e3 if later else None}
         if args.zero_stage == 3:
             # the gather is a change of views; a stale copy would cost one cast
             engine.optimizer.gather_parameters()
@@ -703,7 +721,14 @@ def main(argv=None) -> int:
             "kernel_ms": ({k: round(v, 4) for k, v in other["k_ms"].items()} if other["k_ms"] else None),
         }
     if "accumulate_ms" in head:
-        result["contiguous"] = {"accumulate_ms_per_micro_batch": round(head["accumulate_ms"], 4)}
+        acc = head["accumulate_ms"]
+        result["contiguous"] = {
+            "micro_batches": args.micro_batches,
+            # the hooks of one micro-batch: the first of a window writes the
+            # fp32 sums (6 B/param), the later ones add into them (10 B/param)
+            "accumulate_ms_first_micro_batch": round(acc["first"], 4),
+            "accumulate_ms_later_micro_batch": (round(acc["later"], 4)
+                                                if acc["later"] is not None else None)}
     if "zero3" in head:
         result["zero3"] = head["zero3"]
     if not args.no_cpu_baseline:
