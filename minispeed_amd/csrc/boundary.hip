@@ -94,8 +94,9 @@ constexpr int kStatsBlocks = kStatsBlocksFixed;   // K2 partial slots per group
 // change what it computes, so the shape is free per mode.  Over the 1.3B
 // fp16 gradients (292 segments), in isolation: reading only, 8 waves x
 // runs of 4 tiles x 4 units 0.398 ms (runs of 1 / 2 / 8: 0.59 / 0.43 / 0.43;
-// 4 waves: 0.43; 2 units: 0.41); also writing the fp32 flat gradient, one
-// wave x one tile x 2 units 1.370 ms (4 units: 1.40; runs of 2: 1.43).
+// 4 waves: 0.43; 2 units: 0.41; fp32 gradients 0.822 ms, 2 units 0.841);
+// also writing the fp32 flat gradient, one wave x one tile x 2 units
+// 1.370 ms (4 units: 1.40; runs of 2: 1.43).
 constexpr int kScanTile = MS_SCAN_TILE;
 #ifndef MS_SCAN_WAVES_READ
 #define MS_SCAN_WAVES_READ 8
@@ -337,9 +338,7 @@ __device__ inline float scale_grad(float g, float mul, float div) {
 
 template <class G, bool kFlat, bool kStats, int kScale>
 struct GradScan {
-  // 4-byte gradients read at depth 2 (at 4 their read-only scan spills)
-  static constexpr int kScanDepth =
-      kFlat ? MS_SCAN_DEPTH_FLAT : (G::kBytes == 4 ? 2 : MS_SCAN_DEPTH_READ);
+  static constexpr int kScanDepth = kFlat ? MS_SCAN_DEPTH_FLAT : MS_SCAN_DEPTH_READ;
   static constexpr int kUnit = 16 / G::kBytes;   // elements per 16-byte unit
   // fp16 / bf16 units widen to 32 bytes: staged through LDS so that each
   // store instruction covers 1 KB of whole lines
