@@ -190,6 +190,24 @@ def test_host_argument_errors_return_codes_without_launching():
         _native.check(ETABLE, "probe")
 
 
+def test_integration_stub_matches_the_binding():
+    """The ctypes stub a maintainer copies from INTEGRATION.md declares every
+    entry point with the binding's argument types."""
+    with open(os.path.join(ROOT, "INTEGRATION.md")) as f:
+        text = f.read()
+    short = {"P": "P", "I32": "I32", "I64": "I64", "F": "F", "D": "D"}
+    ctype = {ctypes.c_void_p: "P", ctypes.c_int32: "I32", ctypes.c_int64: "I64",
+             ctypes.c_float: "F", ctypes.c_double: "D"}
+    stubs = re.findall(r"lib\.(\w+)\.argtypes = \[([^\]]*)\]", text)
+    assert {name for name, _ in stubs} >= {"ms_grad_stats", "ms_norm_clip", "ms_fused_adamw",
+                                           "ms_cast_to_model", "ms_accumulate_grads",
+                                           "ms_reduce_tile_stats"}
+    for name, body in stubs:
+        got = [short.get(a.strip(), "P") for a in re.split(r",\s*(?![^(]*\))", body) if a.strip()]
+        want = [ctype.get(t, "P") for t in _native.SIGNATURES[name][1]]
+        assert got == want, name
+
+
 def test_header_constants_match_the_binding():
     with open(HEADER) as f:
         text = f.read()
