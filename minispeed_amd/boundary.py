@@ -1,12 +1,12 @@
-"""The fused boundary step: K1 -> K2 -> K3 on the current HIP stream with one
-device->host read-back.
+"""The fused boundary step: K1 (+ its tile fold) -> K2 -> K3 on the current
+HIP stream with one device->host read-back.
 
 Replaces the unfused sequence of minispeed's
 ``DeepSpeedEngine._take_optimizer_step`` (engine.py:268-322):
 
     flatten_grads            flat.py:196-213       \\
     has_overflow             precision.py:79-87     > K1 per group
-    unscale_grads            flat.py:243-247       /   (+ per-block sumsq)
+    unscale_grads            flat.py:243-247       /   (+ sumsq per 2048-element tile, folded)
     reduce_gradients         stage_1_and_2.py:86-102   identity at world 1
     clip_gradients           stage_1_and_2.py:105-128  K2 (norm, coef, skip)
     FlatAdam.step            optim/adam.py:59-93   \\
