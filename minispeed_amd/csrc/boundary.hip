@@ -87,16 +87,19 @@ constexpr int kAdamThreads = MS_ADAM_THREADS;
 constexpr int kAdamUnroll = MS_ADAM_UNROLL;
 constexpr int kAdamTile = kAdamThreads * kAdamUnroll * 4;          // 512 flat elements (K3)
 constexpr int kStatsBlocks = kStatsBlocksFixed;   // K2 partial slots per group
-// K1: one wave scans a run of consecutive tiles of kScanTile flat indices
-// (searching the segment table once and walking on with a cursor), several
-// waves per block, a few 16-byte units of gradient in flight per lane.
-// Which wave scans a tile, and how many units it has in flight, do not
-// change what it computes, so the shape is free per mode.  Over the 1.3B
-// fp16 gradients (292 segments), in isolation: reading only, 8 waves x
-// runs of 4 tiles x 4 units 0.398 ms (runs of 1 / 2 / 8: 0.59 / 0.43 / 0.43;
-// 4 waves: 0.43; 2 units: 0.41; fp32 gradients 0.822 ms, 2 units 0.841);
-// also writing the fp32 flat gradient, one wave x one tile x 2 units
-// 1.370 ms (4 units: 1.40; runs of 2: 1.43).
+// K1, reading only: one wave scans a run of consecutive tiles of kScanTile
+// flat indices (searching the segment table once and walking on with a
+// cursor), several waves per block, a few 16-byte units of gradient in
+// flight per lane.  Writing the fp32 flat gradient too: four waves per tile,
+// one unit (two for fp32 gradients) per lane, the fp64 sum added up by one
+// wave in the one-wave order.  Which waves scan a tile, and how many units
+// they have in flight, do not change what K1 computes, so the shape is free
+// per mode.  Over the 1.3B fp16 gradients (292 segments), in isolation:
+// reading only, 8 waves x runs of 4 tiles x 4 units 0.398 ms (runs of
+// 1 / 2 / 8: 0.59 / 0.43 / 0.43; 4 waves: 0.43; 2 units: 0.41; fp32
+// gradients 0.822 ms, 2 units 0.841); writing, four waves per tile 1.25-1.27
+// ms (one wave per tile x 2 units: 1.38; two slab sets and one barrier per
+// tile: 1.26-1.28).
 constexpr int kScanTile = MS_SCAN_TILE;
 #ifndef MS_SCAN_WAVES_READ
 #define MS_SCAN_WAVES_READ 8
@@ -107,23 +110,25 @@ constexpr int kScanTile = MS_SCAN_TILE;
 #ifndef MS_SCAN_DEPTH_READ
 #define MS_SCAN_DEPTH_READ 4
 #endif
-#ifndef MS_SCAN_WAVES_FLAT
-#define MS_SCAN_WAVES_FLAT 1
-#endif
-#ifndef MS_SCAN_RUN_FLAT
-#define MS_SCAN_RUN_FLAT 1
-#endif
+// writing the flat gradient: one block per tile, its whole tiles split
+// over the waves (fixed: 256 threads x 8 staged values = one tile); the
+// other tiles, one wave walking them, one unit in flight per lane
+#define MS_SCAN_WAVES_FLAT 4
 #ifndef MS_SCAN_DEPTH_FLAT
-#define MS_SCAN_DEPTH_FLAT 2
+#define MS_SCAN_DEPTH_FLAT 1
 #endif
 constexpr int kScanWavesRead = MS_SCAN_WAVES_READ;
 constexpr int kScanWavesFlat = MS_SCAN_WAVES_FLAT;
 // waves per SIMD K1 is compiled for: left alone, the compiler widens every
 // unit of a round before the (serial) fp64 sum and needs 100+ VGPRs (4
-// waves per SIMD); held to 6 it keeps 48-60 (0.398 ms against 0.433 with
-// 5 and 0.428 with 8)
+// waves per SIMD); reading, held to 6 it keeps 48-60 (0.398 ms against
+// 0.433 with 5 and 0.428 with 8); writing, 8 (1.27 ms against 1.40 with 6,
+// where the walk of the other tiles took 80 VGPRs at 2 units per lane)
 #ifndef MS_SCAN_MIN_WAVES
 #define MS_SCAN_MIN_WAVES 6
+#endif
+#ifndef MS_SCAN_MIN_WAVES_FLAT
+#define MS_SCAN_MIN_WAVES_FLAT 8
 #endif
 constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
 constexpr int kMaxSegs = 1 << 26;
@@ -476,59 +481,169 @@ struct GradScan {
 
 template <bool kFlat>
 constexpr int scan_waves() { return kFlat ? kScanWavesFlat : kScanWavesRead; }
+template <bool kFlat>
+constexpr int scan_min_waves() { return kFlat ? MS_SCAN_MIN_WAVES_FLAT : MS_SCAN_MIN_WAVES; }
 
+// Tile t = [r0, r1) by one wave: walk its segments from the cursor s (left
+// on the segment that holds r1 when that one goes on), then the tile's
+// statistics into its slot.
+template <class Scan, class G, bool kStats>
+__device__ void scan_tile(Scan& sc, const ms_segment_t* segs, int nseg, int& s, int64_t t,
+                          int64_t r0, int64_t r1, int64_t own_begin, int64_t own_end,
+                          double* tsum, uint32_t* tflag, int lane) {
+  for (; s < nseg; ++s) {
+    const ms_segment_t sg = segs[s];
+    const int64_t se = seg_end(sg);
+    const int64_t a = sg.begin > r0 ? sg.begin : r0;
+    const int64_t b = se < r1 ? se : r1;
+    if (a < b) {
+      // split at the owned range so every piece is counted or not
+      const int64_t o0 = own_begin > a ? (own_begin < b ? own_begin : b) : a;
+      const int64_t o1 = own_end < b ? (own_end > o0 ? own_end : o0) : b;
+      if (a < o0) sc.template piece<false>(sg, a, o0, lane);
+      if (o0 < o1) sc.template piece<kStats>(sg, o0, o1, lane);
+      if (o1 < b) sc.template piece<false>(sg, o1, b, lane);
+    }
+    if (se > r1) break;   // it also holds the next tile's first index
+  }
+  if (kStats) {
+    const bool bad = sc.bad || (sc.packed & G::kTop) != 0;
+    const double w = wave_sum(sc.acc);
+    const bool wb = __any(bad);
+    if (lane == 0) {
+      tsum[t] = w;
+      tflag[t] = wb ? 1u : 0u;
+    }
+  }
+}
+
+// Reading only (kFlat false): each wave scans runs of `run` consecutive
+// tiles.  Writing the flat gradient (kFlat): one block of kScanWavesFlat
+// waves per tile.  A whole tile inside one segment with 16-byte aligned
+// storage, starting on a unit boundary of it and owned or not as a whole,
+// is split across the waves: wave w loads, widens and writes units
+// w*k*64 + lane .. (k units per lane), each store covering whole lines; the
+// widened values wait in LDS, and after a barrier wave 0 adds each lane's
+// units l, l + 64, ... in index order — the order one wave scanning the
+// tile alone uses, so the slots get the same bits.  Any other tile is
+// scanned by wave 0 alone, as when reading.
 template <class G, bool kFlat, bool kStats, int kScale>
-__global__ __launch_bounds__(64 * scan_waves<kFlat>(), MS_SCAN_MIN_WAVES) void k_grad_stats(
+__global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) void k_grad_stats(
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
     int64_t end, int64_t own_begin, int64_t own_end, float mul, float div,
     float* __restrict__ flat, double* __restrict__ tsum, uint32_t* __restrict__ tflag,
     int64_t ntiles, int run) {
   constexpr int kWaves = scan_waves<kFlat>();
   using Scan = GradScan<G, kFlat, kStats, kScale>;
-  __shared__ f4 slabs[Scan::kStage ? kWaves : 1][128];
+  __shared__ f4 slabs[kFlat ? kWaves : 1][128];
   const int lane = threadIdx.x & 63;
   // uniform across the wave, and known to be so by the compiler: the tile
   // bounds, the segment search and the piece bookkeeping stay scalar
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // a wave's tiles are uniform across it: no block-level barrier anywhere
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves * run;
-  for (int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * run; t0 < ntiles;
-       t0 += stride) {
-    const int64_t t1 = (t0 + run < ntiles) ? t0 + run : ntiles;
-    // the cursor: the segment holding the next tile's first index
-    int s = find_seg(segs, nseg, begin + t0 * kScanTile);
-    for (int64_t t = t0; t < t1; ++t) {
+  if constexpr (!kFlat) {
+    // a wave's tiles are uniform across it: no block-level barrier
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves * run;
+    for (int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * run; t0 < ntiles;
+         t0 += stride) {
+      const int64_t t1 = (t0 + run < ntiles) ? t0 + run : ntiles;
+      // the cursor: the segment holding the next tile's first index
+      int s = find_seg(segs, nseg, begin + t0 * kScanTile);
+      for (int64_t t = t0; t < t1; ++t) {
+        Scan sc;
+        sc.mul = mul;
+        sc.div = div;
+        sc.begin = begin;
+        sc.flat = (MS_GLOBAL float*)flat;
+        const int64_t r0 = begin + t * kScanTile;
+        const int64_t r1 = (r0 + kScanTile < end) ? r0 + kScanTile : end;
+        scan_tile<Scan, G, kStats>(sc, segs, nseg, s, t, r0, r1, own_begin, own_end, tsum,
+                                   tflag, lane);
+      }
+    }
+  } else {
+    constexpr int kUnit = Scan::kUnit;
+    constexpr int kPerLane = kScanTile / kUnit / (64 * kWaves);   // 1 (2-byte) or 2 (4-byte)
+    static_assert(kPerLane * kUnit == 8, "each lane stages 8 widened values of a tile");
+    __shared__ uint32_t wflag[kWaves];
+    // tiles are uniform across the block, and so are its barriers
+    // Blocks are dealt to the 8 XCDs in turn (block b to XCD b % 8); each
+    // XCD takes a contiguous share of the first nb tiles, so neighbouring
+    // tiles' 12-byte slots leave the same L2 as whole lines (tile t to
+    // block t would write every slot as two partial lines from two L2s:
+    // +40 MB of writes at 1.3B).  A bijection of [0, nb) for any nb.
+    const int64_t nb = gridDim.x, q = nb / 8, rm = nb % 8;
+    const int64_t xcd = blockIdx.x % 8, xi = blockIdx.x / 8;
+    for (int64_t t = xcd * q + (xcd < rm ? xcd : rm) + xi; t < ntiles; t += nb) {
       Scan sc;
       sc.mul = mul;
       sc.div = div;
       sc.begin = begin;
       sc.flat = (MS_GLOBAL float*)flat;
-      sc.slab = (MS_LDS f4*)slabs[Scan::kStage ? wave : 0];
+      sc.slab = (MS_LDS f4*)slabs[wave];
       const int64_t r0 = begin + t * kScanTile;
       const int64_t r1 = (r0 + kScanTile < end) ? r0 + kScanTile : end;
-      for (; s < nseg; ++s) {
-        const ms_segment_t sg = segs[s];
-        const int64_t se = seg_end(sg);
-        const int64_t a = sg.begin > r0 ? sg.begin : r0;
-        const int64_t b = se < r1 ? se : r1;
-        if (a < b) {
-          // split at the owned range so every piece is counted or not
-          const int64_t o0 = own_begin > a ? (own_begin < b ? own_begin : b) : a;
-          const int64_t o1 = own_end < b ? (own_end > o0 ? own_end : o0) : b;
-          if (a < o0) sc.template piece<false>(sg, a, o0, lane);
-          if (o0 < o1) sc.template piece<kStats>(sg, o0, o1, lane);
-          if (o1 < b) sc.template piece<false>(sg, o1, b, lane);
-        }
-        if (se > r1) break;   // it also holds the next tile's first index
+      int s = find_seg(segs, nseg, r0);
+      const ms_segment_t sg = segs[s];
+      const bool owned = own_begin <= r0 && r1 <= own_end;
+      const bool split = r1 - r0 == kScanTile && sg.grad != nullptr && aligned16(sg.grad) &&
+                         sg.begin <= r0 && r1 <= seg_end(sg) &&
+                         ((r0 - sg.begin) & (kUnit - 1)) == 0 &&
+                         aligned16((const void*)(flat + (r0 - begin))) &&
+                         (owned || r1 <= own_begin || own_end <= r0);
+      if (!split) {
+        if (wave == 0)
+          scan_tile<Scan, G, kStats>(sc, segs, nseg, s, t, r0, r1, own_begin, own_end, tsum,
+                                     tflag, lane);
+        continue;
       }
-      if (kStats) {
-        const bool bad = sc.bad || (sc.packed & G::kTop) != 0;
-        const double w = wave_sum(sc.acc);
-        const bool wb = __any(bad);
-        if (lane == 0) {
-          tsum[t] = w;
-          tflag[t] = wb ? 1u : 0u;
+      const char* src = static_cast<const char*>(sg.grad) + (r0 - sg.begin) * G::kBytes;
+      uint32_t w[kPerLane][4];
+#pragma unroll
+      for (int k = 0; k < kPerLane; ++k)
+        load_unit(src + ((wave * kPerLane + k) * 64 + lane) * 16, w[k]);
+      float g[kPerLane][kUnit];
+#pragma unroll
+      for (int k = 0; k < kPerLane; ++k) sc.template widen<false>(w[k], g[k]);
+      if constexpr (Scan::kStage) {
+        // whole-line stores through the slab, which keeps the values
+        sc.put_wave(g[0], r0 + wave * 64 * kUnit, lane);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kPerLane; ++k)
+          sc.put(g[k], r0 + ((wave * kPerLane + k) * 64 + lane) * kUnit, true);
+        if (kStats) {
+          slabs[wave][2 * lane] = f4{g[0][0], g[0][1], g[0][2], g[0][3]};
+          slabs[wave][2 * lane + 1] = f4{g[1][0], g[1][1], g[1][2], g[1][3]};
         }
+      }
+      if constexpr (kStats) {
+        const bool wb = __any((sc.packed & G::kTop) != 0);
+        if (lane == 0) wflag[wave] = wb ? 1u : 0u;
+        __syncthreads();
+        if (wave == 0) {
+          double acc = 0.0;
+          if (owned) {
+#pragma unroll
+            for (int d = 0; d < kWaves; ++d) {
+              const f4 lo = slabs[d][2 * lane], hi = slabs[d][2 * lane + 1];
+              const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+              for (int k = 0; k < 8; ++k) {
+                const double x = static_cast<double>(v[k]);
+                acc = __builtin_fma(x, x, acc);
+              }
+            }
+          }
+          const double tot = wave_sum(acc);
+          if (lane == 0) {
+            uint32_t f = 0;
+#pragma unroll
+            for (int d = 0; d < kWaves; ++d) f |= wflag[d];
+            tsum[t] = tot;
+            tflag[t] = f;
+          }
+        }
+        __syncthreads();   // the slabs and flags are rewritten by the next tile
       }
     }
   }
@@ -984,13 +1099,11 @@ template <class G, int kScale>
 void launch_stats_s(const ms_segment_t* segs, int nseg, int64_t begin, int64_t end, int64_t ob,
                     int64_t oe, float mul, float div, float* flat, double* tsum, uint32_t* tflag,
                     int64_t ntiles, hipStream_t st) {
-  constexpr int kFlatRun = MS_SCAN_RUN_FLAT;
-  constexpr int kFlatTiles = kScanWavesFlat * kFlatRun;
   if (tsum) {
     if (flat) {
-      hipLaunchKernelGGL((k_grad_stats<G, true, true, kScale>), dim3(scan_grid(ntiles, kFlatTiles)),
+      hipLaunchKernelGGL((k_grad_stats<G, true, true, kScale>), dim3(scan_grid(ntiles, 1)),
                          dim3(64 * kScanWavesFlat), 0, st, segs, nseg, begin, end, ob, oe, mul,
-                         div, flat, tsum, tflag, ntiles, kFlatRun);
+                         div, flat, tsum, tflag, ntiles, 1);
     } else {
       // runs of 2 and 4 tiles time alike over 60K-640K tiles, runs of 1 up
       // to 30% slower
@@ -1001,9 +1114,9 @@ void launch_stats_s(const ms_segment_t* segs, int nseg, int64_t begin, int64_t e
                          ntiles, kRun);
     }
   } else {
-    hipLaunchKernelGGL((k_grad_stats<G, true, false, kScale>), dim3(scan_grid(ntiles, kFlatTiles)),
+    hipLaunchKernelGGL((k_grad_stats<G, true, false, kScale>), dim3(scan_grid(ntiles, 1)),
                        dim3(64 * kScanWavesFlat), 0, st, segs, nseg, begin, end, ob, oe, mul, div,
-                       flat, tsum, tflag, ntiles, kFlatRun);
+                       flat, tsum, tflag, ntiles, 1);
   }
 }
 
