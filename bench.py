@@ -1,6 +1,7 @@
 """Boundary-step throughput of minispeed_amd on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload gpt-1.3b | llama3-8b-shard]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+                    [--workload gpt-1.3b | gpt-1.3b-shift3 | llama3-8b-shard | ...]
                     [--grad-dtype fp16] [--mode fused|materialize|contiguous] [--micro-batches 1]
                     [--zero-stage 1]
                     [--state-spacing-gib auto] [--no-cpu-baseline] [--copy-calibration]

@@ -239,27 +239,43 @@ __device__ inline void stq(float* p, const float (&x)[4]) {
 }
 
 template <class D>
+__device__ inline void widen_words(uint32_t w0, uint32_t w1, float (&x)[4]) {
+  x[0] = D::widen(static_cast<uint16_t>(w0 & 0xffffu));
+  x[1] = D::widen(static_cast<uint16_t>(w0 >> 16));
+  x[2] = D::widen(static_cast<uint16_t>(w1 & 0xffffu));
+  x[3] = D::widen(static_cast<uint16_t>(w1 >> 16));
+}
+
+template <class D>
+__device__ inline void narrow_words(const float (&x)[4], uint32_t& w0, uint32_t& w1) {
+  w0 = static_cast<uint32_t>(D::narrow(x[0])) | (static_cast<uint32_t>(D::narrow(x[1])) << 16);
+  w1 = static_cast<uint32_t>(D::narrow(x[2])) | (static_cast<uint32_t>(D::narrow(x[3])) << 16);
+}
+
+// A quad of raw storage (fp16 / bf16 / fp32) at a quad-aligned address;
+// the pointers come from segment tables, hence the address-space casts.
+template <class D>
 __device__ inline void ldq_raw(const void* p, float (&x)[4]) {
   if constexpr (D::kBytes == 2) {
-    const u2 w = __builtin_nontemporal_load(reinterpret_cast<const u2*>(p));
-    x[0] = D::widen(static_cast<uint16_t>(w[0] & 0xffffu));
-    x[1] = D::widen(static_cast<uint16_t>(w[0] >> 16));
-    x[2] = D::widen(static_cast<uint16_t>(w[1] & 0xffffu));
-    x[3] = D::widen(static_cast<uint16_t>(w[1] >> 16));
+    const u2 w = __builtin_nontemporal_load((const MS_GLOBAL u2*)p);
+    widen_words<D>(w[0], w[1], x);
   } else {
-    ldq(static_cast<const float*>(p), x);
+    const f4 v = __builtin_nontemporal_load((const MS_GLOBAL f4*)p);
+    x[0] = v[0];
+    x[1] = v[1];
+    x[2] = v[2];
+    x[3] = v[3];
   }
 }
 
 template <class D>
 __device__ inline void stq_raw(void* p, const float (&x)[4]) {
   if constexpr (D::kBytes == 2) {
-    u2 w;
-    w[0] = static_cast<uint32_t>(D::narrow(x[0])) | (static_cast<uint32_t>(D::narrow(x[1])) << 16);
-    w[1] = static_cast<uint32_t>(D::narrow(x[2])) | (static_cast<uint32_t>(D::narrow(x[3])) << 16);
-    __builtin_nontemporal_store(w, reinterpret_cast<u2*>(p));
+    uint32_t w0, w1;
+    narrow_words<D>(x, w0, w1);
+    __builtin_nontemporal_store(u2{w0, w1}, (MS_GLOBAL u2*)p);
   } else {
-    stq(static_cast<float*>(p), x);
+    __builtin_nontemporal_store(f4{x[0], x[1], x[2], x[3]}, (MS_GLOBAL f4*)p);
   }
 }
 
@@ -269,6 +285,66 @@ __device__ inline bool quad_aligned(const void* p, int64_t elems, int bytes) {
           static_cast<uintptr_t>(4 * bytes - 1)) == 0;
 }
 
+// Quads anywhere an element can be.  Flat layouts pack tensors back to back,
+// so one tensor of odd size puts every later gradient and model copy off
+// the quad alignment of the flat tiles.  kind 0: aligned to the quad;
+// kind 1: 4-byte aligned (one access of 4-byte alignment, which global
+// memory takes for multi-dword loads and stores); kind 2: 2 mod 4 (2-byte
+// elements only), loaded as the three words around it, one element before
+// and one after the quad included, joined with alignbit, and stored as
+// 2 + 4 + 2 bytes.
+typedef float f4w __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u2w __attribute__((ext_vector_type(2), aligned(4)));
+
+__device__ inline int quad_kind(const void* p, int64_t elems, int bytes) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(elems * bytes);
+  if ((a & static_cast<uintptr_t>(4 * bytes - 1)) == 0) return 0;
+  return (a & 3u) == 0 ? 1 : 2;
+}
+
+template <class D>
+__device__ inline void ldq_any(const void* p, int kind, float (&x)[4]) {
+  if (kind == 0) {
+    ldq_raw<D>(p, x);
+  } else if constexpr (D::kBytes == 4) {
+    const f4w v = __builtin_nontemporal_load((const MS_GLOBAL f4w*)p);
+    x[0] = v[0];
+    x[1] = v[1];
+    x[2] = v[2];
+    x[3] = v[3];
+  } else if (kind == 1) {
+    const u2w w = __builtin_nontemporal_load((const MS_GLOBAL u2w*)p);
+    widen_words<D>(w[0], w[1], x);
+  } else {
+    const MS_GLOBAL uint32_t* q = (const MS_GLOBAL uint32_t*)(static_cast<const char*>(p) - 2);
+    const u2w lo = __builtin_nontemporal_load((const MS_GLOBAL u2w*)q);
+    const uint32_t hi = __builtin_nontemporal_load(q + 2);
+    widen_words<D>(__builtin_amdgcn_alignbit(lo[1], lo[0], 16),
+                   __builtin_amdgcn_alignbit(hi, lo[1], 16), x);
+  }
+}
+
+template <class D>
+__device__ inline void stq_any(void* p, int kind, const float (&x)[4]) {
+  if (kind == 0) {
+    stq_raw<D>(p, x);
+  } else if constexpr (D::kBytes == 4) {
+    __builtin_nontemporal_store(f4w{x[0], x[1], x[2], x[3]}, (MS_GLOBAL f4w*)p);
+  } else {
+    uint32_t w0, w1;
+    narrow_words<D>(x, w0, w1);
+    if (kind == 1) {
+      __builtin_nontemporal_store(u2w{w0, w1}, (MS_GLOBAL u2w*)p);
+    } else {
+      MS_GLOBAL char* c = (MS_GLOBAL char*)p;
+      __builtin_nontemporal_store(static_cast<uint16_t>(w0), (MS_GLOBAL uint16_t*)c);
+      __builtin_nontemporal_store(__builtin_amdgcn_alignbit(w1, w0, 16),
+                                  (MS_GLOBAL uint32_t*)(c + 2));
+      __builtin_nontemporal_store(static_cast<uint16_t>(w1 >> 16), (MS_GLOBAL uint16_t*)(c + 6));
+    }
+  }
+}
+
 template <class D>
 __device__ inline typename D::raw load_raw1(const void* base, int64_t k) {
   return ((const MS_GLOBAL typename D::raw*)base)[k];
@@ -276,7 +352,7 @@ __device__ inline typename D::raw load_raw1(const void* base, int64_t k) {
 
 template <class D>
 __device__ inline void store_raw1(void* base, int64_t k, typename D::raw v) {
-  reinterpret_cast<typename D::raw*>(base)[k] = v;
+  ((MS_GLOBAL typename D::raw*)base)[k] = v;
 }
 
 __device__ inline bool aligned16(const void* p) {
@@ -365,22 +441,19 @@ template <class G, bool kFlat, bool kStats, int kScale>
 struct GradScan {
   static constexpr int kScanDepth = kFlat ? MS_SCAN_DEPTH_FLAT : MS_SCAN_DEPTH_READ;
   static constexpr int kUnit = 16 / G::kBytes;   // elements per 16-byte unit
-  // fp16 / bf16 units widen to 32 bytes: staged through LDS so that each
-  // store instruction covers 1 KB of whole lines
-  static constexpr bool kStage = kFlat && kUnit == 8;
   float mul, div;
   int64_t begin;
   MS_GLOBAL float* flat;
-  MS_LDS f4* slab;       // this wave's 2 KB staging slab (kStage)
   double acc = 0.0;
   bool bad = false;      // per-element inf/nan tests
   uint32_t packed = 0;   // packed exponent tests of the vector body
 
+  // element i, its raw value r already loaded (ignored where sg.grad is
+  // null: a zero)
   template <bool kCount>
-  __device__ void element(const ms_segment_t& sg, int64_t i) {
+  __device__ void use1(const ms_segment_t& sg, int64_t i, typename G::raw r) {
     float g = 0.0f;
     if (sg.grad) {
-      const typename G::raw r = load_raw1<G>(sg.grad, i - sg.begin);
       bad |= G::nonfinite(r);
       g = scale_grad<kScale>(G::widen(r), mul, div);
     }
@@ -389,6 +462,11 @@ struct GradScan {
       acc = __builtin_fma(d, d, acc);
     }
     if (kFlat) flat[i - begin] = g;
+  }
+
+  template <bool kCount>
+  __device__ void element(const ms_segment_t& sg, int64_t i) {
+    use1<kCount>(sg, i, sg.grad ? load_raw1<G>(sg.grad, i - sg.begin) : typename G::raw(0));
   }
 
   // One unit: the 16 bytes of raw gradient a lane moves with one load, as
@@ -421,20 +499,6 @@ struct GradScan {
     }
   }
 
-  // The wave's 64 consecutive units, lane l holding unit l, starting at
-  // flat index i0 (16-byte aligned): through the slab, so that each of the
-  // two stores writes 1 KB of whole lines.  Every lane of the wave is active.
-  __device__ void put_wave(const float (&g)[kUnit], int64_t i0, int lane) {
-    slab[2 * lane] = f4{g[0], g[1], g[2], g[3]};
-    slab[2 * lane + 1] = f4{g[4], g[5], g[6], g[7]};
-    __builtin_amdgcn_wave_barrier();
-    const f4 x = slab[lane], y = slab[64 + lane];
-    __builtin_amdgcn_wave_barrier();
-    MS_GLOBAL f4* o = (MS_GLOBAL f4*)(flat + (i0 - begin));
-    __builtin_nontemporal_store(x, o + lane);
-    __builtin_nontemporal_store(y, o + 64 + lane);
-  }
-
   // elements [a, b) of segment sg, all inside (kCount) or all outside the
   // owned range
   template <bool kCount>
@@ -451,51 +515,57 @@ struct GradScan {
       for (int64_t i = a + lane; i < b; i += 64) element<kCount>(sg, i);
       return;
     }
-    for (int64_t i = a + lane; i < au; i += 64) element<kCount>(sg, i);
-    for (int64_t i = bu + lane; i < b; i += 64) element<kCount>(sg, i);
+    // The head [a, au) and the tail [bu, b) hold fewer than kUnit elements
+    // each: one per lane at most.  Each lane adds its head element, its
+    // tail element, then its units.  Reading only, the two elements are
+    // loaded first and added after the first body loads are issued, so a
+    // piece costs one memory round trip, not three; writing (the rare
+    // tiles the split path of k_grad_stats leaves to a walk) they are
+    // added first, which keeps the walk's registers down.
+    const int64_t hi = a + lane, ti = bu + lane;
+    const bool hv = hi < au, tv = ti < b;
+    typename G::raw hr = 0, tr = 0;
+    if constexpr (kFlat) {
+      if (hv) element<kCount>(sg, hi);
+      if (tv) element<kCount>(sg, ti);
+    } else {
+      if (hv) hr = load_raw1<G>(sg.grad, hi - sg.begin);
+      if (tv) tr = load_raw1<G>(sg.grad, ti - sg.begin);
+    }
+    bool ends = !kFlat;   // per lane: added before the lane's first unit
+    auto add_ends = [&] {
+      if (ends) {
+        if (hv) use1<kCount>(sg, hi, hr);
+        if (tv) use1<kCount>(sg, ti, tr);
+        ends = false;
+      }
+    };
     const int64_t nu = (bu - au) / kUnit;
     const char* src = static_cast<const char*>(sg.grad) + (au - sg.begin) * G::kBytes;
     const bool fvec = kFlat && aligned16((const void*)(flat + (au - begin)));
     // Wave order: lane l takes units l, l + 64, ..., so each load
     // instruction of the wave reads one contiguous kilobyte of whole cache
-    // lines.  kScanDepth units are in flight per lane; each lane still takes
-    // its units in increasing order, so its running sum does not depend on
-    // the depth, on the staging or on the mode.
-    int64_t u = lane;
-    if (kStage && fvec) {
-      // rounds in which every lane has all kScanDepth units (a wave-uniform
-      // condition: the slab exchanges data across the wave)
-      for (; (u - lane) + 63 + (kScanDepth - 1) * 64 < nu; u += kScanDepth * 64) {
-        uint32_t w[kScanDepth][4];
+    // lines.  A round has up to kScanDepth units in flight per lane (fewer
+    // at the end of the piece: a lane's last round is partial, never a
+    // string of single units); each lane still takes its units in
+    // increasing order, so its running sum does not depend on the depth or
+    // on the mode.
+    for (int64_t u = lane; u < nu; u += kScanDepth * 64) {
+      uint32_t w[kScanDepth][4];
 #pragma unroll
-        for (int d = 0; d < kScanDepth; ++d) load_unit(src + (u + d * 64) * 16, w[d]);
+      for (int d = 0; d < kScanDepth; ++d)
+        if (u + d * 64 < nu) load_unit(src + (u + d * 64) * 16, w[d]);
+      add_ends();
 #pragma unroll
-        for (int d = 0; d < kScanDepth; ++d) {
-          float g[kUnit];
-          widen<kCount>(w[d], g);
-          put_wave(g, au + (u - lane + d * 64) * kUnit, lane);
-        }
-      }
-    } else {
-      for (; u + (kScanDepth - 1) * 64 < nu; u += kScanDepth * 64) {
-        uint32_t w[kScanDepth][4];
-#pragma unroll
-        for (int d = 0; d < kScanDepth; ++d) load_unit(src + (u + d * 64) * 16, w[d]);
-#pragma unroll
-        for (int d = 0; d < kScanDepth; ++d) {
+      for (int d = 0; d < kScanDepth; ++d) {
+        if (u + d * 64 < nu) {
           float g[kUnit];
           widen<kCount>(w[d], g);
           if (kFlat) put(g, au + (u + d * 64) * kUnit, fvec);
         }
       }
     }
-    for (; u < nu; u += 64) {
-      uint32_t w0[4];
-      load_unit(src + u * 16, w0);
-      float g[kUnit];
-      widen<kCount>(w0, g);
-      if (kFlat) put(g, au + u * kUnit, fvec);
-    }
+    add_ends();
   }
 };
 
@@ -589,27 +659,38 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
     // XCD-ordered: neighbouring tiles' 12-byte slots leave the same L2 as
     // whole lines (tile t in block t would write every slot as two partial
     // lines from two L2s: +40 MB of writes at 1.3B)
-    for (int64_t t = xcd_tile(blockIdx.x, gridDim.x, kXcdChunk); t < ntiles; t += gridDim.x) {
+    const int64_t tfirst = xcd_tile(blockIdx.x, gridDim.x, kXcdChunk);
+    // the segment holding the block's next tile: searched for while the
+    // current tile's loads are in flight (a block takes its tiles one after
+    // another, so the search would otherwise add to every tile's time)
+    int snext = tfirst < ntiles ? find_seg(segs, nseg, begin + tfirst * kScanTile) : 0;
+    for (int64_t t = tfirst; t < ntiles; t += gridDim.x) {
       Scan sc;
       sc.mul = mul;
       sc.div = div;
       sc.begin = begin;
       sc.flat = (MS_GLOBAL float*)flat;
-      sc.slab = (MS_LDS f4*)slabs[wave];
       const int64_t r0 = begin + t * kScanTile;
       const int64_t r1 = (r0 + kScanTile < end) ? r0 + kScanTile : end;
-      int s = find_seg(segs, nseg, r0);
+      int s = snext;
       const ms_segment_t sg = segs[s];
       const bool owned = own_begin <= r0 && r1 <= own_end;
+      // a whole tile inside one segment, storage and flat output 16-byte
+      // aligned, the tile starting on a unit of the storage, owned or not
+      // as a whole
       const bool split = r1 - r0 == kScanTile && sg.grad != nullptr && aligned16(sg.grad) &&
                          sg.begin <= r0 && r1 <= seg_end(sg) &&
                          ((r0 - sg.begin) & (kUnit - 1)) == 0 &&
                          aligned16((const void*)(flat + (r0 - begin))) &&
                          (owned || r1 <= own_begin || own_end <= r0);
+      const int64_t tn = t + gridDim.x;
       if (!split) {
+        // the other tiles (segment edges, missing gradients, segments off
+        // the flat space's unit grid): wave 0 walks them as when reading
         if (wave == 0)
           scan_tile<Scan, G, kStats>(sc, segs, nseg, s, t, r0, r1, own_begin, own_end, tsum,
                                      tflag, lane);
+        if (tn < ntiles) snext = find_seg(segs, nseg, begin + tn * kScanTile);
         continue;
       }
       const char* src = static_cast<const char*>(sg.grad) + (r0 - sg.begin) * G::kBytes;
@@ -617,16 +698,31 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
 #pragma unroll
       for (int k = 0; k < kPerLane; ++k)
         load_unit(src + ((wave * kPerLane + k) * 64 + lane) * 16, w[k]);
+      if (tn < ntiles) snext = find_seg(segs, nseg, begin + tn * kScanTile);
       float g[kPerLane][kUnit];
 #pragma unroll
       for (int k = 0; k < kPerLane; ++k) sc.template widen<false>(w[k], g[k]);
-      if constexpr (Scan::kStage) {
-        // whole-line stores through the slab, which keeps the values
-        sc.put_wave(g[0], r0 + wave * 64 * kUnit, lane);
+      MS_GLOBAL float* o = (MS_GLOBAL float*)flat + (r0 - begin);
+      if constexpr (kUnit == 8) {
+        // 2-byte gradients (units widen to 32 bytes): through the slab, so
+        // that each of the wave's two stores writes one contiguous kilobyte
+        // of whole lines; the slab keeps the values for the sum
+        MS_LDS f4* slab = (MS_LDS f4*)slabs[wave];
+        slab[2 * lane] = f4{g[0][0], g[0][1], g[0][2], g[0][3]};
+        slab[2 * lane + 1] = f4{g[0][4], g[0][5], g[0][6], g[0][7]};
+        __builtin_amdgcn_wave_barrier();
+        const f4 x = slab[lane], y = slab[64 + lane];
+        __builtin_amdgcn_wave_barrier();
+        MS_GLOBAL f4* ow = (MS_GLOBAL f4*)(o + wave * 64 * kUnit);
+        __builtin_nontemporal_store(x, ow + lane);
+        __builtin_nontemporal_store(y, ow + 64 + lane);
       } else {
+        // fp32 gradients: a unit is 16 bytes, lane l's units are already
+        // contiguous across the wave
 #pragma unroll
         for (int k = 0; k < kPerLane; ++k)
-          sc.put(g[k], r0 + ((wave * kPerLane + k) * 64 + lane) * kUnit, true);
+          __builtin_nontemporal_store(f4{g[k][0], g[k][1], g[k][2], g[k][3]},
+                                      (MS_GLOBAL f4*)o + (wave * kPerLane + k) * 64 + lane);
         if (kStats) {
           slabs[wave][2 * lane] = f4{g[0][0], g[0][1], g[0][2], g[0][3]};
           slabs[wave][2 * lane + 1] = f4{g[1][0], g[1][1], g[1][2], g[1][3]};
@@ -637,6 +733,9 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
         if (lane == 0) wflag[wave] = wb ? 1u : 0u;
         __syncthreads();
         if (wave == 0) {
+          // lane l: its units l, l + 64, ... in increasing order, the order
+          // of piece() (slab entry 2l + h: unit d*64 + l, its half h, for
+          // 2-byte gradients; unit (2d + h)*64 + l for fp32)
           double acc = 0.0;
           if (owned) {
 #pragma unroll
@@ -782,11 +881,14 @@ __device__ inline void adamw1(float g, float& p, float& m, float& v,
 }
 
 // One block per kAdamTile-element tile (grid-stride when the grid is
-// clamped).  A tile inside one segment whose grad / model addresses are
-// quad-aligned takes the vector path: each lane streams kAdamUnroll quads
-// in wave order, all loads of the tile first, then the arithmetic and all
-// stores.  Other tiles (segment edges, the tail, misaligned storage) go
-// element by element: lane j takes elements j, j + kAdamThreads, ...
+// clamped), XCD-ordered.  A tile inside one segment takes the vector path:
+// each lane streams kAdamUnroll quads in wave order, all loads of the tile
+// first, then the arithmetic and all stores; the gradient and the model
+// copy move as quads of their tile's kind (quad_kind), so a segment that
+// starts off the quad alignment of the flat space stays on it.  Other tiles
+// (segment edges, the tail, a 2-mod-4 gradient tile at either end of its
+// segment) go element by element: lane j takes elements j, j +
+// kAdamThreads, ...
 template <class G, class M, bool kFlatGrad>
 __global__ __launch_bounds__(kAdamThreads) void k_adamw(
     float* __restrict__ master, float* __restrict__ exp_avg,
@@ -809,9 +911,15 @@ __global__ __launch_bounds__(kAdamThreads) void k_adamw(
     const int s = find_seg(segs, nseg, t0);
     const ms_segment_t seg = segs[s];
     const int64_t so = t0 - seg.begin;   // the tile's offset in the segment
+    // the gradient's and the model copy's quad kinds (every quad of a tile
+    // has its tile's kind); a kind-2 gradient load reads one element before
+    // and one after each quad, inside the segment only where the tile has
+    // a neighbour on both sides
+    const bool rg = !kFlatGrad && seg.grad != nullptr;
+    const int gk = rg ? quad_kind(seg.grad, so, G::kBytes) : 0;
+    const int mk = seg.model != nullptr ? quad_kind(seg.model, so, M::kBytes) : 0;
     const bool fast = t1 - t0 == kAdamTile && so >= 0 && t1 <= seg_end(seg) && arrays_vec &&
-                      (kFlatGrad || seg.grad == nullptr || quad_aligned(seg.grad, so, G::kBytes)) &&
-                      (seg.model == nullptr || quad_aligned(seg.model, so, M::kBytes));
+                      (gk != 2 || (so >= 1 && t1 < seg_end(seg)));
     if (fast) {
       const int64_t tl = t0 - begin;     // the tile's offset in the state arrays
       float g[kAdamUnroll][4], p[kAdamUnroll][4], m[kAdamUnroll][4], v[kAdamUnroll][4];
@@ -820,8 +928,8 @@ __global__ __launch_bounds__(kAdamThreads) void k_adamw(
         const int64_t e = 4 * (static_cast<int64_t>(u) * kAdamThreads + lane);
         if (kFlatGrad) {
           ldq(flat_grad + tl + e, g[u]);
-        } else if (seg.grad) {
-          ldq_raw<G>(static_cast<const char*>(seg.grad) + (so + e) * G::kBytes, g[u]);
+        } else if (rg) {
+          ldq_any<G>(static_cast<const char*>(seg.grad) + (so + e) * G::kBytes, gk, g[u]);
         } else {
 #pragma unroll
           for (int k = 0; k < 4; ++k) g[u][k] = 0.0f;
@@ -841,7 +949,7 @@ __global__ __launch_bounds__(kAdamThreads) void k_adamw(
         stq(master + tl + e, p[u]);
         stq(exp_avg + tl + e, m[u]);
         stq(exp_avg_sq + tl + e, v[u]);
-        if (seg.model) stq_raw<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, p[u]);
+        if (seg.model) stq_any<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, mk, p[u]);
       }
     } else {
       int sl = s;
@@ -887,10 +995,10 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
     const int s = find_seg(segs, nseg, t0);
     const ms_segment_t seg = segs[s];
     const int64_t so = t0 - seg.begin;
-    const bool fast = t1 - t0 == kStreamTile && so >= 0 && t1 <= seg_end(seg) && flat_vec &&
-                      quad_aligned(seg.model, so, M::kBytes);
+    const bool fast = t1 - t0 == kStreamTile && so >= 0 && t1 <= seg_end(seg) && flat_vec;
     if (fast) {
       if (!seg.model) continue;
+      const int mk = quad_kind(seg.model, so, M::kBytes);
       const int64_t tl = t0 - begin;
       float x[kStreamUnroll][4];
 #pragma unroll
@@ -899,7 +1007,7 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
         const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
-        stq_raw<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, x[u]);
+        stq_any<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, mk, x[u]);
       }
     } else {
       int sl = s;
@@ -923,8 +1031,9 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
 // on tile t of the concatenated rows: row r owns tiles [tile0[r],
 // tile0[r+1]), each of kStreamTile elements in wave order, with the
 // non-temporal hint (the accumulation buffer and the gradient are each
-// touched once per micro-batch).  A tile whose addresses are not quad
-// aligned, or the last partial tile of a row, steps element by element.
+// touched once per micro-batch); the slice and the gradient move as quads
+// of their tile's kind (quad_kind).  The last partial tile of a row, and a
+// 2-mod-4 gradient tile at either end of its row, step element by element.
 // With statistics slots (ps / pf of the row) the block also writes the
 // tile's fp64 sum of squares of the unscaled new values (each lane adds
 // its own values in index order, waves reduce with a fixed xor tree, the
@@ -983,20 +1092,22 @@ __global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch
       const double d = static_cast<double>(unscale1(x, L.umode, L.scale, L.inv));
       acc = __builtin_fma(d, d, acc);
     };
-    if (e1 - e0 == kStreamTile && quad_aligned(dst, e0, 4) && quad_aligned(src, e0, D::kBytes)) {
+    // quad kinds as in K3: the accumulation slice (fp32) and the gradient
+    const int dk = quad_kind(dst, e0, 4), sk = quad_kind(src, e0, D::kBytes);
+    if (e1 - e0 == kStreamTile && (sk != 2 || (e0 >= 1 && e1 < n))) {
       float g[kStreamUnroll][4], x[kStreamUnroll][4];
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
         const int64_t i = e0 + static_cast<int64_t>(u * kStreamThreads + lane) * 4;
-        ldq_raw<D>(src + i * D::kBytes, g[u]);
-        if (!first) ldq(dst + i, x[u]);
+        ldq_any<D>(src + i * D::kBytes, sk, g[u]);
+        if (!first) ldq_any<DF32>(dst + i, dk, x[u]);
       }
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
         const int64_t i = e0 + static_cast<int64_t>(u * kStreamThreads + lane) * 4;
 #pragma unroll
         for (int k = 0; k < 4; ++k) x[u][k] = first ? g[u][k] : x[u][k] + g[u][k];
-        stq(dst + i, x[u]);
+        stq_any<DF32>(dst + i, dk, x[u]);
         if (stats) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) count(x[u][k]);

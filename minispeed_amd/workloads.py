@@ -47,6 +47,12 @@ WORKLOADS: Dict[str, dict] = {
                      desc="350M GPT buffer (24 layers, d 1024, vocab 50257)"),
     "gpt-1.3b": dict(shapes=lambda: gpt_shapes(24, 2048, 50257, 2048),
                      desc="1.3B GPT buffer (24 layers, d 2048, vocab 50257, seq 2048)"),
+    # the same after a 3-element tensor: flat layouts pack tensors back to
+    # back, so every later gradient and model copy starts 3 elements off the
+    # 16-byte grid of the flat space (as after an odd-sized vocabulary bias)
+    "gpt-1.3b-shift3": dict(shapes=lambda: [(3,)] + gpt_shapes(24, 2048, 50257, 2048),
+                            desc="1.3B GPT buffer after a 3-element tensor (every later "
+                                 "tensor off the flat space's 16-byte grid)"),
     "llama3-8b": dict(shapes=llama3_8b_shapes,
                       desc="Llama-3-8B (32 layers, d 4096, GQA 32q/8kv, FFN 14336, vocab 128256)"),
 }
