@@ -519,9 +519,11 @@ struct GradScan {
     // each: one per lane at most.  Each lane adds its head element, its
     // tail element, then its units.  Reading only, the two elements are
     // loaded first and added after the first body loads are issued, so a
-    // piece costs one memory round trip, not three; writing (the rare
-    // tiles the split path of k_grad_stats leaves to a walk) they are
-    // added first, which keeps the walk's registers down.
+    // piece costs one memory round trip, not three; writing (the tiles the
+    // split path of k_grad_stats leaves to the walk: segment edges, missing
+    // gradients, tiles off the storage's unit grid) they are added first,
+    // which keeps the registers of that kernel, compiled for 8 waves per
+    // SIMD, within bounds.
     const int64_t hi = a + lane, ti = bu + lane;
     const bool hv = hi < au, tv = ti < b;
     typename G::raw hr = 0, tr = 0;

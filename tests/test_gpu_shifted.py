@@ -4,9 +4,10 @@ The flat layout packs tensors back to back (flat.py:FlatParamGroup, as
 minispeed's), so one tensor of a size that is not a multiple of 8 puts every
 later gradient and model copy off the 16-byte units of K1's tiles and the
 quads of K3's; gradient and model views can also start at any element of
-their storage.  The kernels keep those tiles on their vector paths (K1: the
-four-wave split with a head and a tail, the read walk with its ends loaded
-early; K3 / K4 / K5: quads of any alignment).  Checked here:
+their storage.  The kernels keep those tiles on vector paths (K1: the walk
+of a tile's head, tail and units, its ends loaded with the first units,
+rounds predicated; when writing the flat gradient, the one-wave walk; K3 /
+K4 / K5: quads of any alignment).  Checked here:
 
 * K1 for every head length and dtype: the flat gradient bit for bit against
   the widened, scaled gradients, every tile flag exactly, tile sums within
