@@ -19,7 +19,9 @@ K4 / K5: quads of any alignment).  Checked here:
   and model element must be too);
 * K4's model copies of every kind against torch's casts, K5's gradient at
   2 mod 4 bytes against the fp32 sum;
-* an engine on a shifted GPT-like list against the oracle, step by step.
+* an engine on a shifted GPT-like list against the oracle, step by step,
+  and ZeRO-3 (parameters gathered as views at odd offsets of one buffer)
+  against stage 0 bit for bit.
 """
 
 from __future__ import annotations
@@ -262,3 +264,37 @@ def test_engine_on_a_shifted_list_against_the_oracle(dtype, stage):
     master = g.data.cpu()
     for (off, p), n in zip(g._offsets, g._numels):
         np.testing.assert_array_equal(bits(p.detach().reshape(-1)), bits(master[off:off + n].to(tdt)))
+
+
+def test_zero3_on_a_shifted_list_equals_stage0():
+    """ZeRO-3 gathers the parameters as views of one model-dtype buffer, here
+    at odd element offsets (K3's and K4's model stores of every kind): the
+    masters and the gathered parameters equal stage 0's bit for bit."""
+    sizes = [3, 4099, 5, 8192, 77, 6000, 1]
+    out = {}
+    for stage in (0, 3):
+        gen = torch.Generator().manual_seed(4)
+        init = [torch.randn(n, generator=gen) * 0.02 for n in sizes]
+        params = [nn.Parameter(t.to(DEV)) for t in init]
+        module = nn.ParameterList(params)
+        cfg = {"train_micro_batch_size_per_gpu": 1, "gradient_accumulation_steps": 1,
+               "gradient_clipping": 1.0, "dtype": "fp16",
+               "fp16": {"enabled": True, "loss_scale": 0, "initial_scale_power": 8},
+               "optimizer": {"type": "AdamW", "params": {"lr": 1e-3, "weight_decay": 0.01}},
+               "zero_optimization": {"stage": stage}, "steps_per_print": 1000}
+        engine = ms.initialize(model=module, model_parameters=list(module), config=cfg)
+        for _ in range(3):
+            if stage == 3:
+                engine.optimizer.gather_parameters()
+            grads = [(torch.randn(n, generator=gen) * 1e-2 * 2.0 ** 8).half() for n in sizes]
+            for p, gr in zip(params, grads):
+                p.grad = gr.to(DEV)
+            engine.micro_steps += 1
+            assert engine.step() is True
+        if stage == 3:
+            engine.optimizer.gather_parameters()
+        out[stage] = (engine.flat_groups[0].data.detach().cpu().clone(),
+                      [p.detach().cpu().clone() for p in params])
+    np.testing.assert_array_equal(bits(out[3][0]), bits(out[0][0]))
+    for a, b in zip(out[3][1], out[0][1]):
+        np.testing.assert_array_equal(bits(a), bits(b))
