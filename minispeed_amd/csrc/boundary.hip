@@ -121,9 +121,10 @@ constexpr int kScanWavesRead = MS_SCAN_WAVES_READ;
 constexpr int kScanWavesFlat = MS_SCAN_WAVES_FLAT;
 // waves per SIMD K1 is compiled for: left alone, the compiler widens every
 // unit of a round before the (serial) fp64 sum and needs 100+ VGPRs (4
-// waves per SIMD); reading, held to 6 it keeps 48-60 (0.398 ms against
-// 0.433 with 5 and 0.428 with 8); writing, 8 (1.27 ms against 1.40 with 6,
-// where the walk of the other tiles took 80 VGPRs at 2 units per lane)
+// waves per SIMD); reading, held to 6 it keeps 56-72 (0.39-0.40 ms; with
+// the walk before its ends were loaded early, 0.398 ms against 0.433 with
+// 5 and 0.428 with 8); writing, 8 (1.27 ms against 1.40 with 6, where the
+// walk of the other tiles took 80 VGPRs at 2 units per lane)
 #ifndef MS_SCAN_MIN_WAVES
 #define MS_SCAN_MIN_WAVES 6
 #endif
