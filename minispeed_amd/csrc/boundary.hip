@@ -253,19 +253,16 @@ __device__ inline void narrow_words(const float (&x)[4], uint32_t& w0, uint32_t&
   w1 = static_cast<uint32_t>(D::narrow(x[2])) | (static_cast<uint32_t>(D::narrow(x[3])) << 16);
 }
 
-// A quad of raw storage (fp16 / bf16 / fp32) at a quad-aligned address;
-// the pointers come from segment tables, hence the address-space casts.
+// A quad of raw storage (fp16 / bf16 / fp32) at a quad-aligned address
+// (generic pointers, flat_* instructions: K3 over 1.3B params 5.75-5.81 ms
+// against 5.81-5.82 with global_* ones, alternating runs on one box).
 template <class D>
 __device__ inline void ldq_raw(const void* p, float (&x)[4]) {
   if constexpr (D::kBytes == 2) {
-    const u2 w = __builtin_nontemporal_load((const MS_GLOBAL u2*)p);
+    const u2 w = __builtin_nontemporal_load(reinterpret_cast<const u2*>(p));
     widen_words<D>(w[0], w[1], x);
   } else {
-    const f4 v = __builtin_nontemporal_load((const MS_GLOBAL f4*)p);
-    x[0] = v[0];
-    x[1] = v[1];
-    x[2] = v[2];
-    x[3] = v[3];
+    ldq(static_cast<const float*>(p), x);
   }
 }
 
@@ -274,9 +271,9 @@ __device__ inline void stq_raw(void* p, const float (&x)[4]) {
   if constexpr (D::kBytes == 2) {
     uint32_t w0, w1;
     narrow_words<D>(x, w0, w1);
-    __builtin_nontemporal_store(u2{w0, w1}, (MS_GLOBAL u2*)p);
+    __builtin_nontemporal_store(u2{w0, w1}, reinterpret_cast<u2*>(p));
   } else {
-    __builtin_nontemporal_store(f4{x[0], x[1], x[2], x[3]}, (MS_GLOBAL f4*)p);
+    stq(static_cast<float*>(p), x);
   }
 }
 
@@ -296,6 +293,11 @@ __device__ inline bool quad_aligned(const void* p, int64_t elems, int bytes) {
 // 2 + 4 + 2 bytes.
 typedef float f4w __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u2w __attribute__((ext_vector_type(2), aligned(4)));
+
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
 
 __device__ inline int quad_kind(const void* p, int64_t elems, int bytes) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(elems * bytes);
@@ -998,11 +1000,25 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
     const int s = find_seg(segs, nseg, t0);
     const ms_segment_t seg = segs[s];
     const int64_t so = t0 - seg.begin;
-    const bool fast = t1 - t0 == kStreamTile && so >= 0 && t1 <= seg_end(seg) && flat_vec;
-    if (fast) {
+    const bool whole = t1 - t0 == kStreamTile && so >= 0 && t1 <= seg_end(seg) && flat_vec;
+    const int64_t tl = t0 - begin;
+    if (whole && quad_aligned(seg.model, so, M::kBytes)) {
       if (!seg.model) continue;
+      float x[kStreamUnroll][4];
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u)
+        ldq(flat + tl + 4 * (static_cast<int64_t>(u) * kStreamThreads + lane), x[u]);
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
+        stq_raw<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, x[u]);
+      }
+    } else if (whole && seg.model) {
+      // a model copy off the quads of the flat tiles (a segment shifted by
+      // an earlier tensor of odd size, or a view at an odd offset): quads
+      // of its kind; a separate branch, so that the aligned tiles above
+      // keep their code (folding the kind into it cost the 8.03B cast 6%)
       const int mk = quad_kind(seg.model, so, M::kBytes);
-      const int64_t tl = t0 - begin;
       float x[kStreamUnroll][4];
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u)
@@ -1095,27 +1111,44 @@ __global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch
       const double d = static_cast<double>(unscale1(x, L.umode, L.scale, L.inv));
       acc = __builtin_fma(d, d, acc);
     };
-    // quad kinds as in K3: the accumulation slice (fp32) and the gradient
+    // quad kinds as in K3: the accumulation slice (fp32) and the gradient;
+    // the tile's code is compiled twice, all-aligned quads and any kind, so
+    // that the common tile runs no per-quad dispatch
     const int dk = quad_kind(dst, e0, 4), sk = quad_kind(src, e0, D::kBytes);
-    if (e1 - e0 == kStreamTile && (sk != 2 || (e0 >= 1 && e1 < n))) {
+    auto quads = [&](auto aligned) {
+      constexpr bool kAligned = decltype(aligned)::value;
       float g[kStreamUnroll][4], x[kStreamUnroll][4];
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
         const int64_t i = e0 + static_cast<int64_t>(u * kStreamThreads + lane) * 4;
-        ldq_any<D>(src + i * D::kBytes, sk, g[u]);
-        if (!first) ldq_any<DF32>(dst + i, dk, x[u]);
+        if constexpr (kAligned) {
+          ldq_raw<D>(src + i * D::kBytes, g[u]);
+          if (!first) ldq(dst + i, x[u]);
+        } else {
+          ldq_any<D>(src + i * D::kBytes, sk, g[u]);
+          if (!first) ldq_any<DF32>(dst + i, dk, x[u]);
+        }
       }
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
         const int64_t i = e0 + static_cast<int64_t>(u * kStreamThreads + lane) * 4;
 #pragma unroll
         for (int k = 0; k < 4; ++k) x[u][k] = first ? g[u][k] : x[u][k] + g[u][k];
-        stq_any<DF32>(dst + i, dk, x[u]);
+        if constexpr (kAligned)
+          stq(dst + i, x[u]);
+        else
+          stq_any<DF32>(dst + i, dk, x[u]);
         if (stats) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) count(x[u][k]);
         }
       }
+    };
+    if (e1 - e0 == kStreamTile && (sk != 2 || (e0 >= 1 && e1 < n))) {
+      if (dk == 0 && sk == 0)
+        quads(BoolC<true>{});
+      else
+        quads(BoolC<false>{});
     } else {
       for (int64_t i = e0 + lane; i < e1; i += kStreamThreads) {
         const float g1 = D::widen(load_raw1<D>(src, i));
