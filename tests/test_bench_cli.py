@@ -72,3 +72,19 @@ def test_measured_traffic_only_for_the_measured_configuration():
                   ("k3", "gpt-1.3b", "fp16", "materialize", 32),
                   ("k3", "gpt2-124m", "fp16", "fused", 32)):
         assert bench.traffic_for(*other) is None
+
+
+def test_shifted_workload_is_the_headline_list_behind_three_elements():
+    from minispeed_amd.workloads import numel, shapes_of
+
+    base, shifted = shapes_of("gpt-1.3b"), shapes_of("gpt-1.3b-shift3")
+    assert shifted[0] == (3,) and shifted[1:] == base
+    assert numel(shifted) == numel(base) + 3 == 1_315_723_267
+    # every later tensor starts 3 elements past a multiple of 8 of the flat space
+    off = 3
+    for s in shifted[1:]:
+        assert off % 8 == 3
+        n = 1
+        for x in s:
+            n *= x
+        off += n
