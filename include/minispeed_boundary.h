@@ -79,7 +79,11 @@ enum {
  *           the cast of the updated fp32 master (flat.py:148-154), or NULL
  *           when nothing is written (padding; ZeRO-3 while not gathered).
  * A table passed to a kernel lives in device memory, is sorted by `begin`,
- * and tiles the kernel's range exactly (no gaps, no overlap).
+ * and tiles the kernel's range exactly (no gaps, no overlap).  `begin` and
+ * the two pointers may have any element alignment (a tensor of odd size
+ * shifts every later segment of a packed flat layout): results do not
+ * depend on it; speed does somewhat (16-byte aligned storage starting on
+ * the flat space's 16-byte grid is the fastest case).
  * Replaces the per-parameter (offset, numel, param) list walked by
  * FlatParamGroup.flatten_grads / copy_flat_to_model (flat.py:78-86, 196-213,
  * 133-154).
