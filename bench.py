@@ -454,6 +454,32 @@ def bench_hbm_ceilings(args) -> dict:
         out[name] = best
         log(f"[bench] {name}: {best['gbps']:.0f} GB/s ({best})")
 
+    # K3's access pattern (AdamW arithmetic, fp16 g and copy) on layouts of
+    # the state: p, m, v in three 32 GiB windows (the engine's arena), the
+    # same with XCD-ordered blocks, and the three interleaved per tile of T
+    # elements in one array
+    probe.msp_adam_layout.restype = ctypes.c_int
+    probe.msp_adam_layout.argtypes = [ctypes.POINTER(P), P, P, ctypes.c_int64, ctypes.c_int32,
+                                      ctypes.c_int32, P]
+    n_el = nbytes // 4
+    arena[:3 * nbytes].zero_()           # room for the interleaved state in window 0
+    layouts = {"windows": ([at[0], at[1], at[2]], 0, 0),
+               "windows_xcd_1024": ([at[0], at[1], at[2]], 0, 1024),
+               "interleaved_512": ([at[0]] * 3, 512, 0),
+               "interleaved_2048": ([at[0]] * 3, 2048, 0)}
+    k3_layout = {}
+    for name, (state, inter, chunk) in layouts.items():
+        sp = (P * 3)(*state)
+
+        def fn():
+            rc = probe.msp_adam_layout(sp, at[3], at[4], n_el, inter, chunk, stream)
+            if rc != 0:
+                raise RuntimeError(f"msp_adam_layout failed with {rc}")
+        ms = median_ms(fn)
+        k3_layout[name] = {"ms": round(ms, 4), "gbps": round(28 * n_el / (ms * 1e-3) / 1e9, 1)}
+        log(f"[bench] K3 layout {name}: {ms:.4f} ms")
+    out["k3_layout"] = dict(k3_layout, note=f"{n_el} elements, 28 B each")
+
     lib = _native.load()
     n = 1 << 30
     g = torch.full((n,), 0.5, dtype=torch.float16, device=dev)

@@ -111,6 +111,62 @@ void launch_u(const ProbeArgs& a, int grid, int threads, int wave, int nt_load, 
     launch_nt<U, false>(a, grid, threads, nt_load, nt_store, s);
 }
 
+// ---- K3's access pattern on a chosen state layout (msp_adam_layout)
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+__device__ inline int64_t layout_tile(int64_t b, int64_t nb, int64_t chunk) {
+  if (chunk <= 0) return b;
+  const int64_t g0 = b / (8 * chunk) * (8 * chunk);
+  const int64_t r = (nb - g0 < 8 * chunk) ? nb - g0 : 8 * chunk;
+  const int64_t x = b % 8, xi = (b - g0) / 8, q = r / 8, rm = r % 8;
+  return g0 + x * q + (x < rm ? x : rm) + xi;
+}
+
+__device__ inline float h2f(uint32_t w, int hi) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? w >> 16 : w)));
+}
+
+__device__ inline uint32_t f2h2(float a, float b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+}
+
+template <int T>
+__global__ __launch_bounds__(128) void k_adam_layout(float* p0, float* m0, float* v0,
+                                                     const uint32_t* g, uint32_t* copy,
+                                                     int64_t n, int chunk) {
+  const int64_t tile = layout_tile(blockIdx.x, gridDim.x, chunk);
+  const int64_t i = tile * 512 + 4 * static_cast<int64_t>(threadIdx.x);
+  if (i >= n) return;
+  float *pp, *mp, *vp;
+  if (T == 0) {
+    pp = p0 + i;
+    mp = m0 + i;
+    vp = v0 + i;
+  } else {
+    pp = p0 + (i / T) * 3 * T + i % T;
+    mp = pp + T;
+    vp = pp + 2 * T;
+  }
+  const u2 gw = __builtin_nontemporal_load(reinterpret_cast<const u2*>(g + i / 2));
+  f4 p = __builtin_nontemporal_load(reinterpret_cast<const f4*>(pp));
+  f4 m = __builtin_nontemporal_load(reinterpret_cast<const f4*>(mp));
+  f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(vp));
+  const float gv[4] = {h2f(gw[0], 0), h2f(gw[0], 1), h2f(gw[1], 0), h2f(gw[1], 1)};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    m[k] = __builtin_fmaf(gv[k], 0.1f, m[k] * 0.9f);
+    v[k] = __builtin_fmaf(0.001f * gv[k], gv[k], v[k] * 0.999f);
+    p[k] = p[k] + (-1e-3f * m[k]) / (sqrtf(v[k]) + 1e-8f);
+  }
+  __builtin_nontemporal_store(p, reinterpret_cast<f4*>(pp));
+  __builtin_nontemporal_store(m, reinterpret_cast<f4*>(mp));
+  __builtin_nontemporal_store(v, reinterpret_cast<f4*>(vp));
+  __builtin_nontemporal_store(u2{f2h2(p[0], p[1]), f2h2(p[2], p[3])},
+                              reinterpret_cast<u2*>(copy + i / 2));
+}
+
 }  // namespace
 
 extern "C" {
@@ -149,6 +205,36 @@ int msp_stream(const void* const* rd, int32_t nread, void* const* wr, int32_t nw
     case 2: launch_u<2>(a, static_cast<int>(g), threads, wave, nt_load, nt_store, s); break;
     case 4: launch_u<4>(a, static_cast<int>(g), threads, wave, nt_load, nt_store, s); break;
     default: launch_u<8>(a, static_cast<int>(g), threads, wave, nt_load, nt_store, s); break;
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : static_cast<int>(e);
+}
+
+int msp_adam_layout(float* const* state, const void* g, void* copy, int64_t n,
+                    int32_t interleave, int32_t xcd_chunk, void* stream) {
+  if (state == nullptr || g == nullptr || copy == nullptr || n <= 0 || n % 512 != 0) return -1;
+  if (interleave != 0 && interleave != 512 && interleave != 1024 && interleave != 2048 &&
+      interleave != 4096)
+    return -1;
+  if (interleave != 0 && n % interleave != 0) return -1;
+  if (xcd_chunk < 0 || n / 512 > 0x7fffffff) return -1;
+  const int narr = interleave ? 1 : 3;
+  for (int k = 0; k < narr; ++k)
+    if (state[k] == nullptr || (reinterpret_cast<uintptr_t>(state[k]) & 15u)) return -1;
+  if ((reinterpret_cast<uintptr_t>(g) & 7u) || (reinterpret_cast<uintptr_t>(copy) & 7u)) return -1;
+  float* p = state[0];
+  float* m = interleave ? state[0] : state[1];
+  float* v = interleave ? state[0] : state[2];
+  const auto* gw = static_cast<const uint32_t*>(g);
+  auto* cw = static_cast<uint32_t*>(copy);
+  const dim3 grid(static_cast<unsigned>(n / 512)), block(128);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (interleave) {
+    case 0: hipLaunchKernelGGL(k_adam_layout<0>, grid, block, 0, s, p, m, v, gw, cw, n, xcd_chunk); break;
+    case 512: hipLaunchKernelGGL(k_adam_layout<512>, grid, block, 0, s, p, m, v, gw, cw, n, xcd_chunk); break;
+    case 1024: hipLaunchKernelGGL(k_adam_layout<1024>, grid, block, 0, s, p, m, v, gw, cw, n, xcd_chunk); break;
+    case 2048: hipLaunchKernelGGL(k_adam_layout<2048>, grid, block, 0, s, p, m, v, gw, cw, n, xcd_chunk); break;
+    default: hipLaunchKernelGGL(k_adam_layout<4096>, grid, block, 0, s, p, m, v, gw, cw, n, xcd_chunk); break;
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : static_cast<int>(e);

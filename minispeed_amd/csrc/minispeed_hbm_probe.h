@@ -12,7 +12,7 @@
 extern "C" {
 #endif
 
-#define MSP_ABI_VERSION 1
+#define MSP_ABI_VERSION 2
 #define MSP_MAX_ARRAYS 4
 
 int msp_abi_version(void);
@@ -36,6 +36,24 @@ int msp_abi_version(void);
 int msp_stream(const void* const* rd, int32_t nread, void* const* wr, int32_t nwrite,
                int64_t nvec, int32_t threads, int32_t unroll, int32_t wave, int32_t grid,
                int32_t nt_load, int32_t nt_store, uint32_t* sink, void* stream);
+
+/*
+ * K3's access pattern on a chosen layout of the AdamW state: per element
+ * read g (fp16), p, m, v (fp32), update them with AdamW arithmetic, write
+ * p, m, v and an fp16 copy; one 128-thread block per 512 elements, one
+ * quad per lane, non-temporal hints on every stream.
+ *   state[0..2] [dev] : p, m, v (interleave 0), or state[0] alone holding
+ *                       [tile of T][p T | m T | v T] (interleave T)
+ *   g, copy [dev]     : n fp16 elements each
+ *   n                 : elements, a multiple of 512 and of T
+ *   interleave        : 0, or T in {512, 1024, 2048, 4096}
+ *   xcd_chunk         : 0 = block b on tile b; c > 0 = the 8 XCDs (blocks
+ *                       dealt in turn) each take c consecutive tiles of
+ *                       every group of 8c
+ * Returns 0, -1 for a bad argument (nothing launched), or a hipError_t.
+ */
+int msp_adam_layout(float* const* state, const void* g, void* copy, int64_t n,
+                    int32_t interleave, int32_t xcd_chunk, void* stream);
 
 #ifdef __cplusplus
 }
