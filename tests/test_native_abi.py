@@ -248,3 +248,35 @@ def test_pointer_walk_extension_loads_and_defers_host_tensors():
     assert _walk.record_streams([None, torch.zeros(2), params[0]], 1, 0, 0) == 0
     with pytest.raises(TypeError):
         _walk.record_streams([3], 1, 0, 0)
+
+
+def test_probe_library_abi_and_refusals():
+    """libms_hbm_probe.so (bench.py --hbm-ceilings only): its ABI version,
+    every function its header declares, and bad arguments refused in host
+    code before anything is launched."""
+    here = os.path.dirname(os.path.abspath(_native.library_path()))
+    path = os.path.join(here, "libms_hbm_probe.so")
+    if not os.path.exists(path):
+        pytest.skip("probe library not built (python -m minispeed_amd.build)")
+    lib = ctypes.CDLL(path)
+    header = open(os.path.join(here, "csrc", "minispeed_hbm_probe.h")).read()
+    version = int(re.search(r"#define MSP_ABI_VERSION (\d+)", header).group(1))
+    lib.msp_abi_version.restype = ctypes.c_int
+    assert lib.msp_abi_version() == version == 2
+    for name in re.findall(r"^int (msp_\w+)\(", header, re.M):
+        assert hasattr(lib, name), name
+    P = ctypes.c_void_p
+    lib.msp_adam_layout.restype = ctypes.c_int
+    lib.msp_adam_layout.argtypes = [ctypes.POINTER(P), P, P, ctypes.c_int64, ctypes.c_int32,
+                                    ctypes.c_int32, P]
+    state = (P * 3)(16, 32, 48)
+    ok = dict(state=state, g=64, copy=128, n=4096, inter=0, chunk=0)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return lib.msp_adam_layout(a["state"], a["g"], a["copy"], a["n"], a["inter"], a["chunk"],
+                                   None)
+    for bad in (dict(n=0), dict(n=4095), dict(inter=256), dict(inter=4096, n=2048 * 3),
+                dict(chunk=-1), dict(g=None), dict(copy=66), dict(state=(P * 3)(16, 0, 48)),
+                dict(state=(P * 3)(16, 40, 48))):
+        assert call(**bad) == -1, bad
