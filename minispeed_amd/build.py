@@ -6,11 +6,10 @@
   ABI (no torch headers), compiled with hipcc;
 * ``_walk.so``: a small host-only Python extension (g++, torch and pybind11
   headers) that collects the device addresses of parameter gradients and
-  storages for the segment tables;
-* ``libms_hbm_probe.so``: streaming probes for bench.py's --hbm-ceilings
-  mode (measurement only; nothing on the boundary path loads it).
+  storages for the segment tables.
 
-All are written next to this file so that they travel with the source tree.
+Both are written next to this file so that they travel with the source tree.
+(bench.py's streaming probes are built by ``bench_probes/build.py``.)
 """
 
 from __future__ import annotations
@@ -109,26 +108,8 @@ def build_walk(verbose: bool = False) -> str:
     return WALK_OUTPUT
 
 
-PROBE_SOURCE = os.path.join(PKG_DIR, "csrc", "hbm_probe.hip")
-PROBE_OUTPUT = os.path.join(PKG_DIR, "libms_hbm_probe.so")
-
-
-def build_probe(verbose: bool = False) -> str:
-    """Compile ``libms_hbm_probe.so``, the streaming probes of bench.py's
-    --hbm-ceilings mode (always)."""
-    tmp = PROBE_OUTPUT + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{os.path.dirname(PROBE_SOURCE)}", PROBE_SOURCE, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}{proc.stderr}")
-    os.replace(tmp, PROBE_OUTPUT)
-    return PROBE_OUTPUT
-
-
 def build_all(verbose: bool = False) -> List[str]:
-    return [build(verbose=verbose), build_walk(verbose=verbose), build_probe(verbose=verbose)]
+    return [build(verbose=verbose), build_walk(verbose=verbose)]
 
 
 def main(argv=None) -> int:

@@ -254,12 +254,12 @@ def test_probe_library_abi_and_refusals():
     """libms_hbm_probe.so (bench.py --hbm-ceilings only): its ABI version,
     every function its header declares, and bad arguments refused in host
     code before anything is launched."""
-    here = os.path.dirname(os.path.abspath(_native.library_path()))
+    here = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "bench_probes")
     path = os.path.join(here, "libms_hbm_probe.so")
     if not os.path.exists(path):
-        pytest.skip("probe library not built (python -m minispeed_amd.build)")
+        pytest.skip("probe library not built (python -m bench_probes.build)")
     lib = ctypes.CDLL(path)
-    header = open(os.path.join(here, "csrc", "minispeed_hbm_probe.h")).read()
+    header = open(os.path.join(here, "minispeed_hbm_probe.h")).read()
     version = int(re.search(r"#define MSP_ABI_VERSION (\d+)", header).group(1))
     lib.msp_abi_version.restype = ctypes.c_int
     assert lib.msp_abi_version() == version == 2
