@@ -108,6 +108,9 @@ def parse(argv=None):
                     help="CPU baseline sample (0: the whole workload, ~1 minute at 1.3B)")
     ap.add_argument("--hbm-ceilings", action="store_true",
                     help="measure streaming-bandwidth reference points instead of the boundary step")
+    ap.add_argument("--no-extra-workloads", dest="extra_workloads", action="store_false",
+                    help="with the default headline workload: skip the short runs of the other "
+                         "single-GPU configurations (GPT-2 124M, 350M, the Llama-3-8B shard)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (a counter yardstick for rocprofv3 --pmc)")
     return ap.parse_args(argv)
@@ -209,6 +212,63 @@ def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
     }
 
 
+# the other single-GPU configurations: (workload, ZeRO stage) of the
+# reported short runs next to the headline, with what they stand for
+EXTRA_WORKLOADS = (
+    ("gpt2-124m", 2, "GPT-2 small (124M params, 148 tensors), fp16 grads x 2^16, ZeRO-2"),
+    ("gpt-350m", 0, "350M GPT (24 layers, d 1024, 292 tensors), fp16 grads x 2^16, ZeRO-0"),
+)
+EXTRA_STEPS, EXTRA_WARMUP = 20, 5
+
+
+def extra_workloads(args, run_engine, gen, dev, gdt, mult) -> dict:
+    """Short runs of the boundary step on the other single-GPU
+    configurations, each through the engine with its default placement
+    (step time back to back, kernel times from HIP events), and the
+    Llama-3-8B shard at component level.  The bar of each is 80% of the
+    8 TB/s peak at the bytes its step moves."""
+    import numpy as np
+    import torch
+
+    from minispeed_amd.workloads import numel, shapes_of
+
+    out = {}
+    for name, stage, desc in EXTRA_WORKLOADS:
+        shapes = shapes_of(name)
+        n = numel(shapes)
+        sets = []
+        old = args.zero_stage
+        args.zero_stage = stage
+        try:
+            r = run_engine("auto", EXTRA_STEPS, True, shapes=shapes, grad_sets=sets, warmup=EXTRA_WARMUP)
+        finally:
+            args.zero_stage = old
+        del sets
+        torch.cuda.empty_cache()
+        gbps = 30 * n / (r["ms_step"] * 1e-3) / 1e9
+        out[name] = {"desc": desc, "params": n, "zero_stage": stage, "steps": EXTRA_STEPS,
+                     "ms_per_step": round(r["ms_step"], 4),
+                     "value": round(n / (r["ms_step"] * 1e-3) / 1e9, 3), "unit": "Gparams/s",
+                     "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_GBPS, 4),
+                     "bar_ms_at_80pct": round(30 * n / (0.8 * PEAK_GBPS * 1e9) * 1e3, 4),
+                     "kernel_ms": {k: round(v, 4) for k, v in r["k_ms"].items()},
+                     "k3_gbps": round(28 * n / (r["k_ms"]["k3"] * 1e-3) / 1e9, 1),
+                     "state_placement": r["placement"]}
+        log(f"[bench] {name}: {r['ms_step']:.4f} ms/step, {gbps:.0f} GB/s")
+    shard_args = argparse.Namespace(**vars(args))
+    shard_args.steps, shard_args.warmup = EXTRA_STEPS, EXTRA_WARMUP
+    sh = bench_llama_shard(shard_args)
+    s_params = sh["config"]["shard_params"]
+    out["llama3-8b-shard"] = {
+        "desc": sh["config"]["workload"], "params": s_params, "model_params": sh["config"]["model_params"],
+        "steps": EXTRA_STEPS, "ms_per_step": sh["ms_per_step"], "value": sh["value"], "unit": "Gparams/s",
+        "hbm_gbps": sh["hbm_gbps"], "hbm_frac": round(sh["hbm_gbps"] / PEAK_GBPS, 4),
+        "bar_ms_at_80pct": round(30 * s_params / (0.8 * PEAK_GBPS * 1e9) * 1e3, 4),
+        "kernel_ms": sh["kernel_ms"], "cast_on_gather": sh["cast_on_gather"]}
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_llama_shard(args) -> dict:
     """One rank's 1/8 ZeRO-3 shard of Llama-3-8B (rank 3 of 8) plus the full
     cast-on-gather, at component level through the C ABI.
@@ -224,7 +284,7 @@ def bench_llama_shard(args) -> dict:
     import torch
 
     from minispeed_amd import _native
-    from minispeed_amd.boundary import LaunchTimer, adamw_params
+    from minispeed_amd.boundary import HostWait, LaunchTimer, adamw_params
     from minispeed_amd.flat import AUTO_SPACING, FlatLayout, check_table, state_buffers
     from minispeed_amd.workloads import shapes_of
 
@@ -267,7 +327,7 @@ def bench_llama_shard(args) -> dict:
     tflag = torch.empty(ntiles, dtype=torch.int32, device=dev)
     scal = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, device=dev)
     host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
-    k2_done = torch.cuda.Event()
+    k2_done = HostWait(dev)
     timer = LaunchTimer()
 
     def step(k: int, timed: bool) -> None:
@@ -285,7 +345,7 @@ def bench_llama_shard(args) -> dict:
         _native.check(lib.ms_norm_clip(psum.data_ptr(), pflag.data_ptr(), nb, 1, 1, 1.0, 0, 1.0,
                                        0, 0, 1000, 1.0, 2.0 ** 24, scal.data_ptr(), host.data_ptr(),
                                        stream), "ms_norm_clip")
-        k2_done.record()
+        k2_done.record(stream)
         tok = t.start("k3") if t else None
         _native.check(lib.ms_fused_adamw(master.data_ptr(), m.data_ptr(), v.data_ptr(), None,
                                          tdev.data_ptr(), len(table), _native.DTYPE_BF16,
@@ -293,7 +353,7 @@ def bench_llama_shard(args) -> dict:
                                          scal.data_ptr(), stream), "ms_fused_adamw")
         if t:
             t.stop(tok)
-        k2_done.synchronize()
+        k2_done.wait()
 
     for k in range(args.warmup):
         step(k, False)
@@ -386,7 +446,7 @@ def bench_hbm_ceilings(args) -> dict:
 
     dev = torch.device("cuda", 0)
     stream = _native.stream_handle(dev)
-    probe = ctypes.CDLL(os.path.join(ROOT, "minispeed_amd", "libms_hbm_probe.so"))
+    probe = ctypes.CDLL(os.path.join(ROOT, "bench_probes", "libms_hbm_probe.so"))
     P = ctypes.c_void_p
     probe.msp_stream.restype = ctypes.c_int
     probe.msp_stream.argtypes = [ctypes.POINTER(P), ctypes.c_int32, ctypes.POINTER(P), ctypes.c_int32,
@@ -541,11 +601,13 @@ def main(argv=None) -> int:
     mult = 2.0 ** 16 if args.grad_dtype == "fp16" else 1.0
     grad_sets = []
 
-    def run_engine(spacing, steps: int, kernel_timing: bool) -> dict:
+    def run_engine(spacing, steps: int, kernel_timing: bool, shapes=shapes, grad_sets=grad_sets,
+                   warmup: int = args.warmup) -> dict:
         """Build an engine with this state placement, warm it up and time
         ``steps`` boundaries back to back and then one at a time.  As in
         training, the engine (and its state) is built before the gradients
-        exist; two gradient sets are made once and shared by every run."""
+        exist; two gradient sets are made once and shared by every run of
+        one tensor list."""
         params = [nn.Parameter(torch.randn(*s, generator=gen, device=dev) * 0.02) for s in shapes]
         module = nn.ParameterList(params)
         engine = ms.initialize(model=module, model_parameters=list(module),
@@ -554,12 +616,10 @@ def main(argv=None) -> int:
         while len(grad_sets) < 2:
             grad_sets.append([(torch.randn(*s, generator=gen, device=dev) * (1e-3 * mult)).to(gdt)
                               for s in shapes])
-        g0 = engine.flat_groups[0]
-        st0 = engine.optimizer.state[0]
-        same = st0["exp_avg"].untyped_storage().data_ptr() == g0.data.untyped_storage().data_ptr()
-        window = (st0["exp_avg"].data_ptr() - g0.data.data_ptr()) / 2 ** 30 if same else 0.0
+        where = engine.state_placement
+        window = where.window / 2 ** 30
         torch.cuda.synchronize()
-        log(f"[bench] state placement {spacing!r}: window {window:g} GiB; warming up")
+        log(f"[bench] state placement {spacing!r}: window {window:g} GiB, {where}; warming up")
         gather_s, accum_s = [], []   # accum_s: (micro-batch index, seconds)
 
         def attach(k: int, measure: bool = False) -> None:
@@ -599,7 +659,7 @@ def main(argv=None) -> int:
             if not engine.step():
                 raise RuntimeError("boundary step was skipped (unexpected overflow)")
 
-        for k in range(args.warmup):
+        for k in range(warmup):
             attach(k)
             boundary()
         torch.cuda.synchronize()
@@ -645,6 +705,9 @@ def main(argv=None) -> int:
             f"{'back to back' if back_to_back else 'one at a time'}, "
             f"{sum(step_s) * 1e3:.3f} ms one at a time")
         out = {"ms_step": elapsed / steps * 1e3, "step_s": step_s, "window_gib": window,
+               "placement": {"arena_gib": round(where.arena_bytes / 2 ** 30, 3),
+                             "held_gib": round(where.held_bytes / 2 ** 30, 3),
+                             "returned_to_allocator_gib": round(where.returned_bytes / 2 ** 30, 3)},
                "timing": "back to back" if back_to_back else "one at a time",
                "k_ms": ({k: float(np.mean(timer.durations_ms(k))) for k in ("k1", "k2", "k3")}
                         if kernel_timing else None)}
@@ -720,6 +783,7 @@ def main(argv=None) -> int:
             "mode": args.mode,
             "state_spacing_gib": args.state_spacing_gib,
             "state_window_gib": head["window_gib"],
+            "state_placement": head["placement"],
             "clip": 1.0,
             "bytes_per_param": b1 + b3,
         },
@@ -759,6 +823,12 @@ def main(argv=None) -> int:
                                                 if acc["later"] is not None else None)}
     if "zero3" in head:
         result["zero3"] = head["zero3"]
+    if args.extra_workloads and args.workload == "gpt-1.3b" and args.mode == "fused" \
+            and args.zero_stage == 1 and args.grad_dtype == "fp16" and args.state_spacing_gib == "auto":
+        # the other single-GPU configurations, short runs of the same step
+        del grad_sets[:]
+        torch.cuda.empty_cache()
+        result["workloads"] = extra_workloads(args, run_engine, gen, dev, gdt, mult)
     if not args.no_cpu_baseline:
         del grad_sets
         torch.cuda.empty_cache()

@@ -252,6 +252,7 @@ def stream_handle(device: torch.device) -> int:
 # the kernels it brackets; the elapsed time between two such events is valid
 # once the stream has been synchronised.
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+HIP_EVENT_DISABLE_TIMING = 0x2
 _hip: Optional[ctypes.CDLL] = None
 
 
@@ -271,8 +272,9 @@ def hip_runtime() -> ctypes.CDLL:
             hip.hipEventRecord.argtypes = [_P, _P]
             hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(_F), _P, _P]
             hip.hipEventDestroy.argtypes = [_P]
+            hip.hipEventSynchronize.argtypes = [_P]
             for fn in (hip.hipEventCreateWithFlags, hip.hipEventRecord, hip.hipEventElapsedTime,
-                       hip.hipEventDestroy):
+                       hip.hipEventDestroy, hip.hipEventSynchronize):
                 fn.restype = ctypes.c_int
             _hip = hip
     return _hip

@@ -65,6 +65,36 @@ def adamw_params(
     )
 
 
+class HostWait:
+    """The host's wait for K2: an event recorded on the stream right after
+    K2, without the system-scope release a default event performs (K2 makes
+    its write to pinned host memory visible before it ends, with a
+    system-scope fence of its own) and without a timestamp.  A default event
+    there costs the next kernel a cache write-back: a 5.5 us gap between K2
+    and K3."""
+
+    def __init__(self, device: torch.device):
+        self._hip = _native.hip_runtime()
+        ev = ctypes.c_void_p()
+        with torch.cuda.device(device):     # an event belongs to the device current at creation
+            _native.hip_check(self._hip.hipEventCreateWithFlags(
+                ctypes.byref(ev),
+                _native.HIP_EVENT_DISABLE_SYSTEM_FENCE | _native.HIP_EVENT_DISABLE_TIMING),
+                "hipEventCreateWithFlags")
+        self._ev = ev.value
+
+    def record(self, stream: int) -> None:
+        _native.hip_check(self._hip.hipEventRecord(self._ev, stream), "hipEventRecord")
+
+    def wait(self) -> None:
+        _native.hip_check(self._hip.hipEventSynchronize(self._ev), "hipEventSynchronize")
+
+    def __del__(self):
+        hip, ev = getattr(self, "_hip", None), getattr(self, "_ev", None)
+        if hip is not None and ev:
+            hip.hipEventDestroy(ev)
+
+
 class Workspace:
     """Device scratch of the boundary step (no allocation per step)."""
 
@@ -84,10 +114,10 @@ class Workspace:
         self._tile_streams: set = set()
         # K2 also writes its result here (pinned host memory the device
         # writes directly), so the read-back is a wait on an event recorded
-        # after K2: no copy, and K3, queued behind K2, keeps running while
-        # the host does its bookkeeping
+        # after K2 (HostWait): no copy, and K3, queued behind K2, keeps
+        # running while the host does its bookkeeping
         self.host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
-        self._k2_done = torch.cuda.Event()
+        self._k2_done = HostWait(device)
         self._stream: Optional[torch.cuda.Stream] = None   # stream of the last boundary
 
     def partial_ptrs(self, g: int):
@@ -134,12 +164,12 @@ class Workspace:
     def start_readback(self) -> None:
         """Mark the end of K2 (just launched on the current stream with
         ``host`` as its host-side output)."""
-        self._k2_done.record(self._stream)
+        self._k2_done.record(self._stream.cuda_stream)
 
     def finish_readback(self) -> _native.StepScalars:
         """Wait for K2 (later kernels on the stream keep running) and read
         the scalars it wrote to pinned host memory."""
-        self._k2_done.synchronize()
+        self._k2_done.wait()
         return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
 
 
@@ -281,10 +311,7 @@ def run_boundary(
         gdtype = dtype if gl.grad_dtype is None else gl.grad_dtype
         flat_out = None
         if materialize_flat_grad:
-            if g.grad is None:
-                g.grad = torch.empty(g.numel_padded, dtype=torch.float32, device=device)
-            flat_out = g.grad
-            g._grad_dirty = True
+            flat_out = g.flat_grad_for_overwrite()      # K1 writes every element
         lo, hi = g.own_range
         gbytes = 4 if gdtype == _native.DTYPE_F32 else 2
         psum, pflag = ws.partial_ptrs(gi)

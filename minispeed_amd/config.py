@@ -16,7 +16,7 @@ minispeed config drives this package unchanged:
 One section is specific to this package and ignored by minispeed:
 
     "hip_boundary": {"materialize_flat_grad": false, "contiguous_gradients": false,
-                     "state_spacing_gib": "auto"}
+                     "state_spacing_gib": "auto", "stage3_gather_reuse": false}
 
 With ``materialize_flat_grad`` the ragged-grad kernel also writes the fp32
 flat gradient buffer and the AdamW kernel reads it back (36 B/param for half
@@ -30,18 +30,27 @@ backward.  This changes the numerics (fp32 instead of half accumulation), so
 it is not bitwise minispeed and is off by default.
 
 ``state_spacing_gib`` places the fp32 masters, exp_avg and exp_avg_sq of all
-groups: with a number of GiB they are views of one allocation (the state
-arena) of three windows of that size, array j at the start of window j; 0
-gives three separate allocations; "auto" (the default) uses 32 GiB windows
-for states of 256 MiB to 32 GiB per array when the 96 GiB arena takes at
-most half of the free device memory, and separate allocations otherwise.
-On MI355X the arena makes the fused AdamW kernel 10-15% faster than
-separate allocations (1.3B params: 5.7-5.9 against 6.5-6.9 ms; 124M params:
-0.54 against 0.61-0.63 ms), at the price of the windows' unused part (about
-80 GiB at 1.3B params, 6 GiB at 8B).  The
-placement changes no result.  The tensors are then views of one
-allocation: ``torch.save`` them through ``state_dict()`` / the checkpoint
-functions (which copy them out), not directly.
+groups: with a number of GiB they lie in one allocation (the state arena) of
+three windows of that size, array j at the start of window j; 0 gives three
+separate allocations; "auto" (the default) uses 32 GiB windows for states of
+256 MiB to 32 GiB per array when the 96 GiB arena takes at most half of the
+free device memory, and separate allocations otherwise.  On MI355X the
+fused AdamW kernel streams the three arrays 10-15% faster when they lie far
+apart in physical memory (1.3B params: 5.7-5.8 against 6.2-6.9 ms for
+separate allocations; 124M params: 0.54 against 0.61-0.63 ms).  The arena is
+carved through torch's caching allocator: the state holds only its own
+bytes, and the rest of the arena goes back to the allocator as free blocks
+that later tensors of the process are served from (``engine.state_placement``
+and an INFO log line at ``initialize`` give the figures).  The placement
+changes no result.
+
+``stage3_gather_reuse`` (opt-in): at world size 1 a ZeRO-3 gather casts the
+masters into the parameters every time, as minispeed does (stage_3.py:67-86),
+1.3 ms at 1.3B params.  With the option the gather skips that cast when the
+parameters' buffer already holds the cast of the current masters (nothing
+has written the masters or the parameters since), which torch's version
+counters tell, except for a write through a freed placeholder's ``.data``:
+that one survives the next gather, where minispeed would overwrite it.
 """
 
 from __future__ import annotations
@@ -98,6 +107,7 @@ class DeepSpeedConfig:
         hip = _section(raw, "hip_boundary")
         self.materialize_flat_grad = bool(hip.get("materialize_flat_grad", False))
         self.contiguous_gradients = bool(hip.get("contiguous_gradients", False))
+        self.stage3_gather_reuse = bool(hip.get("stage3_gather_reuse", False))
         spacing = hip.get("state_spacing_gib", "auto")
         if spacing == "auto":
             self.state_spacing_bytes = -1          # flat.AUTO_SPACING
@@ -207,7 +217,8 @@ class DeepSpeedConfig:
         return getattr(torch, _TORCH_DTYPE_NAMES[self.dtype])
 
     _SHOWN = ("dtype", "zero_stage", "gas", "micro_batch", "gradient_clipping",
-              "state_spacing_bytes", "materialize_flat_grad", "contiguous_gradients")
+              "state_spacing_bytes", "materialize_flat_grad", "contiguous_gradients",
+              "stage3_gather_reuse")
 
     def __repr__(self) -> str:
         shown = ", ".join(f"{k}={getattr(self, k, None)!r}" for k in self._SHOWN)

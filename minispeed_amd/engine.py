@@ -94,6 +94,8 @@ class DeepSpeedEngine:
             zero_stage=self.config.zero_stage, device=self.device,
             state_spacing=self.config.state_spacing_bytes,
         )
+        # where the masters and moments were put (flat.place_state)
+        self.state_placement = self.flat_groups[0].state_placement
         for g in self.flat_groups:
             g.copy_model_to_flat()
 
@@ -109,6 +111,8 @@ class DeepSpeedEngine:
                 g.partition_params()
 
         self.optimizer = build_zero_optimizer(self.flat_groups, option_groups, zero_stage=self.config.zero_stage)
+        if self.config.zero_stage >= 3:
+            self.optimizer.gather_reuse = self.config.stage3_gather_reuse
         self.contiguous: Optional[ContiguousGradients] = None
         if self.config.contiguous_gradients:
             self.contiguous = ContiguousGradients(
@@ -268,6 +272,8 @@ class DeepSpeedEngine:
     def load_state_dict(self, state_dict):
         self.optimizer.gather_parameters()
         self.module.load_state_dict(state_dict)
+        # where the masters and moments were put (flat.place_state)
+        self.state_placement = self.flat_groups[0].state_placement
         for g in self.flat_groups:
             g.copy_model_to_flat()
 

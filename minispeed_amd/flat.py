@@ -26,6 +26,7 @@ flat range exactly, gaps and padding being rows with NULL pointers.
 from __future__ import annotations
 
 import logging
+import os
 from typing import Iterable, List, Optional, Sequence, Tuple
 
 import numpy as np
@@ -313,43 +314,172 @@ def auto_window(sizes: Sequence[Sequence[int]], free_bytes: Optional[int] = None
     return _AUTO_WINDOW
 
 
+class StatePlacement:
+    """Where :func:`place_state` put the masters and moments.
+
+    ``window``: the arena's window in bytes, 0 for separate allocations.
+    ``arena_bytes``: size of the arena's allocation (0 without one).
+    ``held_bytes``: device memory the state buffers hold (their 2 MiB slots).
+    ``returned_bytes``: the arena's part that is not state, handed back to
+    torch's caching allocator as free blocks (0 when the arena could not be
+    carved and stays one tensor).
+    """
+
+    __slots__ = ("window", "arena_bytes", "held_bytes", "returned_bytes")
+
+    def __init__(self, window: int = 0, arena_bytes: int = 0, held_bytes: int = 0,
+                 returned_bytes: int = 0):
+        self.window = window
+        self.arena_bytes = arena_bytes
+        self.held_bytes = held_bytes
+        self.returned_bytes = returned_bytes
+
+    def __repr__(self) -> str:
+        return (f"StatePlacement(window={self.window}, arena_bytes={self.arena_bytes}, "
+                f"held_bytes={self.held_bytes}, returned_bytes={self.returned_bytes})")
+
+
+_CARVE_TRIES = 64
+
+
+def _expandable_segments() -> bool:
+    conf = ",".join(os.environ.get(k, "") for k in ("PYTORCH_HIP_ALLOC_CONF", "PYTORCH_CUDA_ALLOC_CONF",
+                                                   "PYTORCH_ALLOC_CONF"))
+    return "expandable_segments:true" in conf.replace(" ", "").lower()
+
+
+def _take_at(addr: int, nbytes: int, device: torch.device,
+             spare: List[torch.Tensor]) -> Optional[torch.Tensor]:
+    """A uint8 tensor of ``nbytes`` from torch's caching allocator that starts
+    at ``addr``, or None.  The allocator serves a request from the smallest
+    free block that fits, splitting it from its start; blocks it picks
+    elsewhere are held in ``spare`` (released by the caller) so that the
+    next request moves on to a larger one."""
+    for _ in range(_CARVE_TRIES):
+        t = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        if t.data_ptr() == addr:
+            return t
+        spare.append(t)
+    return None
+
+
+def _carve(total: int, slots: Sequence[Tuple[int, int]],
+           device: torch.device) -> Optional[List[torch.Tensor]]:
+    """Tensors for ``slots`` ((byte offset, bytes), sorted, disjoint, 2 MiB
+    multiples) at those offsets of one fresh allocation of ``total`` bytes,
+    with every byte between and after them handed back to torch's caching
+    allocator as free blocks of that allocation; None (nothing kept) when
+    the allocator does not serve the requests from that allocation.
+
+    The allocation is made whole, then freed into the allocator's pool (the
+    allocator keeps it: its memory stays where the driver put it), and the
+    slots and the gaps between them are requested in address order: each
+    request splits the remaining free block from its start.  Then the gap
+    tensors are dropped, so later tensors of the process (activations,
+    gradients) can be served from the gaps."""
+    arena = torch.empty(total, dtype=torch.uint8, device=device)
+    base = arena.data_ptr()
+    del arena
+    spare: List[torch.Tensor] = []
+    gaps: List[torch.Tensor] = []
+    out: List[torch.Tensor] = []
+    cursor = 0
+    try:
+        for off, nbytes in slots:
+            if off > cursor:
+                gap = _take_at(base + cursor, off - cursor, device, spare)
+                if gap is None:
+                    return None
+                gaps.append(gap)
+            t = _take_at(base + off, nbytes, device, spare)
+            if t is None:
+                return None
+            out.append(t)
+            cursor = off + nbytes
+        return out
+    finally:
+        del spare, gaps
+
+
 def state_buffers(sizes: Sequence[Sequence[int]], device: torch.device,
                   window: int) -> List[List[torch.Tensor]]:
-    """Zeroed fp32 buffers, ``sizes[g][j]`` elements for array j of group g.
+    """The buffers of :func:`place_state` without the placement record."""
+    return place_state(sizes, device, window)[0]
+
+
+def place_state(sizes: Sequence[Sequence[int]], device: torch.device,
+                window: int) -> Tuple[List[List[torch.Tensor]], StatePlacement]:
+    """Zeroed fp32 buffers, ``sizes[g][j]`` elements for array j of group g,
+    and where they were put.
 
     With ``window`` 0 they are separate allocations; ``AUTO_SPACING`` picks
-    the window with :func:`auto_window`.  With a window they are views of
-    one allocation, the state arena (:func:`arena_layout`): array j of every
-    group starts at ``j * window``, the groups back to back at the same
-    offsets in every window.  The fused AdamW kernel reads and writes the
-    masters, exp_avg and exp_avg_sq at the same flat index in lockstep, and
-    on MI355X that streams fastest when the three lie far apart in
-    *physical* HBM, which the runtime decides when it backs an allocation
-    with memory.  Measured on the 1.3B-param state (three 4.9 GiB arrays),
-    K3's time in fresh bench processes: separate allocations 6.5-6.9 ms,
-    one packed allocation 6.7-6.8 ms, three 32 GiB windows 5.73-6.06 ms
-    (every box tried), 16 GiB windows 5.71-5.73 ms on some boxes and
-    6.43-6.55 ms on others.  Columns larger than the window are allocated
+    the window with :func:`auto_window`.  With a window they lie in one
+    allocation of three windows, the state arena (:func:`arena_layout`):
+    array j of every group starts at ``j * window``, the groups back to back
+    at the same offsets in every window.  The fused AdamW kernel reads and
+    writes the masters, exp_avg and exp_avg_sq at the same flat index in
+    lockstep, and on MI355X that streams fastest when the three lie far
+    apart in *physical* HBM.  The driver backs an allocation with naturally
+    aligned power-of-two blocks, so windows of 32 GiB at the start of a 96
+    GiB allocation (a 64 GiB and a 32 GiB block) are 32 GiB apart in
+    physical memory too.  Measured on the 1.3B-param state (three 4.9 GiB
+    arrays), K3 in the arena 5.7-5.8 ms; three separate allocations 6.2-6.9
+    ms; one allocation holding the three back to back 6.0-6.3 ms, with
+    staggers of 4 KiB to 1.5 GiB between them 6.2-6.3 ms; windows of 6 to
+    28 GiB inside one 64 GiB block 6.0-6.3 ms on one box.
+
+    The arena is carved through torch's caching allocator (:func:`_carve`):
+    the state keeps only its slots, and the rest of the 96 GiB -- the
+    windows' unused part -- goes back to the allocator as free blocks that
+    any later tensor allocated on the same stream can use.  If the
+    allocator does not serve the slots from the arena (another free block
+    of the pool fits better each time, or expandable segments), the arena
+    stays one tensor.  Columns larger than the window are allocated
     separately, and so is everything when the device lacks the free memory
     (with a log line).  The placement changes no result.
     """
     def plain() -> List[List[torch.Tensor]]:
         return [[torch.zeros(int(n), dtype=torch.float32, device=device) for n in row] for row in sizes]
 
+    def held(rows) -> int:
+        return sum(_round_up(4 * int(n), _ARENA_ALIGN) for row in rows for n in row)
+
     if window == AUTO_SPACING:
         window = auto_window(sizes, torch.cuda.mem_get_info(device)[0])
     layout = arena_layout(sizes, window)
     if layout is None:
-        return plain()
+        return plain(), StatePlacement(held_bytes=held(sizes))
+    if _expandable_segments():
+        _log.warning("state arena skipped: torch's expandable segments map memory page by page, "
+                     "so the arena's windows would not be apart in physical memory; allocating the "
+                     "masters and moments separately")
+        return plain(), StatePlacement(held_bytes=held(sizes))
     starts, total = layout
+    window = total // len(sizes[0])          # rounded up to 2 MiB by arena_layout
     free, _ = torch.cuda.mem_get_info(device)
     if free < total + _ARENA_SLACK_BYTES:
         _log.warning("state arena of %.1f GiB does not fit in %.1f GiB free device memory; "
                      "allocating the masters and moments separately", total / 2**30, free / 2**30)
-        return plain()
+        return plain(), StatePlacement(held_bytes=held(sizes))
+    slots = sorted((a, _round_up(4 * int(n), _ARENA_ALIGN))
+                   for row, row_starts in zip(sizes, starts) for n, a in zip(row, row_starts))
+    carved = _carve(total, slots, device)
+    if carved is not None:
+        by_start = {a: t for (a, _), t in zip(slots, carved)}
+        bufs = [[by_start[a][:4 * int(n)].view(torch.float32).zero_() for n, a in zip(row, row_starts)]
+                for row, row_starts in zip(sizes, starts)]
+        kept = sum(b for _, b in slots)
+        placement = StatePlacement(window, total, kept, total - kept)
+        _log.info("state arena: masters and moments in %d windows of %.0f GiB; %.2f GiB held by "
+                  "the state, %.2f GiB returned to torch's allocator", len(sizes[0]),
+                  window / 2**30, kept / 2**30, (total - kept) / 2**30)
+        return bufs, placement
+    _log.warning("state arena: torch's allocator did not serve the state slots from the arena; "
+                 "keeping the whole %.0f GiB arena as one tensor", total / 2**30)
     arena = torch.empty(total, dtype=torch.uint8, device=device)
-    return [[arena[a:a + 4 * int(n)].view(torch.float32).zero_() for n, a in zip(row, row_starts)]
+    bufs = [[arena[a:a + 4 * int(n)].view(torch.float32).zero_() for n, a in zip(row, row_starts)]
             for row, row_starts in zip(sizes, starts)]
+    return bufs, StatePlacement(window, total, total, 0)
 
 
 def arena_layout(sizes: Sequence[Sequence[int]],
@@ -425,6 +555,7 @@ class FlatParamGroup:
                 t.dtype != torch.float32 or t.device.type != "cuda" or t.device.index != index
                 for t in state):
             raise ValueError(f"state buffers must be fp32 on cuda:{index} with {sizes} elements")
+        self.state_placement = StatePlacement(held_bytes=sum(_round_up(4 * n, _ARENA_ALIGN) for n in sizes))
         self._master_shard: Optional[torch.Tensor] = None
         if sizes[0] != self.numel_padded:
             # the masters shrink to the owned range in partition_params
@@ -433,7 +564,10 @@ class FlatParamGroup:
         else:
             self.data, exp_avg, exp_avg_sq = state
         self._moments: Optional[Tuple[torch.Tensor, torch.Tensor]] = (exp_avg, exp_avg_sq)
-        self.grad: Optional[torch.Tensor] = (
+        # True while `grad` is logically zero but its memory still holds the
+        # last boundary's values (see the `grad` property)
+        self._grad_stale = False
+        self._grad: Optional[torch.Tensor] = (
             None if zero_stage >= 3 else torch.zeros(self.numel_padded, dtype=torch.float32, device=device)
         )
         self.grad_shard: Optional[torch.Tensor] = (
@@ -457,8 +591,9 @@ class FlatParamGroup:
         # changed without that cast
         self._model_token: Optional[Tuple[int, int, int]] = None
         # True while `grad` / `grad_shard` may hold non-zero values; lets
-        # zero_grad skip clearing buffers the fused boundary never wrote.
+        # zero_grad skip clearing buffers nothing wrote.
         self._grad_dirty = False
+        self._shard_dirty = False
         self._tables = {}
         self._rows = None   # static (begin, numel) rows of the whole-range table
         self._device_index = device.index if device.index is not None else torch.cuda.current_device()
@@ -791,6 +926,33 @@ class FlatParamGroup:
         return table
 
     # ----------------------------------------------------------- grads
+    @property
+    def grad(self) -> Optional[torch.Tensor]:
+        """The fp32 flat gradient (flat.py:61-73).  After ``zero_grad`` it
+        reads as zeros, as in the reference; the clearing itself waits until
+        something reads the buffer, because the boundary that writes it
+        next (the flattening scan) overwrites every element anyway.  A
+        training loop that never looks at ``grad`` therefore pays no
+        clearing pass (4 B/param per step)."""
+        if self._grad_stale:
+            self._grad.zero_()
+            self._grad_stale = False
+        return self._grad
+
+    @grad.setter
+    def grad(self, value: Optional[torch.Tensor]) -> None:
+        self._grad = value
+        self._grad_stale = False
+
+    def flat_grad_for_overwrite(self) -> torch.Tensor:
+        """The flat gradient buffer (allocated if absent) for a kernel that
+        writes every element of it: a pending clear is dropped, not done."""
+        if self._grad is None:
+            self._grad = torch.empty(self.numel_padded, dtype=torch.float32, device=self.device)
+        self._grad_stale = False
+        self._grad_dirty = True
+        return self._grad
+
     def release_grads(self) -> None:
         for p in self.params:
             p.grad = None
@@ -800,8 +962,7 @@ class FlatParamGroup:
         """``param.grad`` -> fp32 flat ``grad`` (flat.py:196-213); params
         without a gradient contribute zeros, every floating dtype is widened
         exactly, ``param.grad`` is released."""
-        if self.grad is None:
-            self.grad = torch.empty(self.numel_padded, dtype=torch.float32, device=self.device)
+        flat = self.flat_grad_for_overwrite()
         # the C++ walk of the gradients; a gradient in another floating dtype
         # makes every address point into one exactly widened fp32 buffer
         ptrs, keep, gdtype = self.grad_pointers()
@@ -811,11 +972,10 @@ class FlatParamGroup:
         table = self.boundary_table(0, self.numel_padded, ptrs, None, gbytes)
         ptr, n = self.table("flatten").upload(table)
         rc = _native.load().ms_grad_stats(
-            ptr, n, gdtype, 0, self.numel_padded, 0, 0, 0, 1.0, self.grad.data_ptr(),
+            ptr, n, gdtype, 0, self.numel_padded, 0, 0, 0, 1.0, flat.data_ptr(),
             None, None, 0, None, None, 0, _native.stream_handle(self.device),
         )
         _native.check(rc, "ms_grad_stats(flatten)")
-        self._grad_dirty = True
         self.release_grads()
         # the gradients may have been allocated on another stream: their
         # memory must not be reused there before the kernel above has read it
@@ -824,16 +984,18 @@ class FlatParamGroup:
 
     @torch.no_grad()
     def zero_grad(self) -> None:
-        """flat.py:215-223; buffers the fused boundary never wrote are
-        already zero and are not cleared again."""
-        if self.grad is not None:
+        """flat.py:215-223.  Buffers nothing wrote are already zero and are
+        not cleared again; a written ``grad`` is cleared when it is next
+        read (the ``grad`` property), ``grad_shard`` at once."""
+        if self._grad is not None:
             if self.zero_stage >= 3:
                 self.grad = None
             elif self._grad_dirty:
-                self.grad.zero_()
-        if self.grad_shard is not None and self._grad_dirty:
+                self._grad_stale = True
+        if self.grad_shard is not None and self._shard_dirty:
             self.grad_shard.zero_()
         self._grad_dirty = False
+        self._shard_dirty = False
 
     def grad_for_shard(self) -> torch.Tensor:
         if self.grad_shard is not None:
@@ -853,10 +1015,10 @@ class FlatParamGroup:
     @torch.no_grad()
     def unscale_grads(self, scale: float) -> None:
         """``grad /= scale`` over the whole flat gradient (flat.py:243-247)."""
-        if scale == 1.0 or self.grad is None:
-            return
+        if scale == 1.0 or self._grad is None or self._grad_stale:
+            return      # nothing, or zeros: dividing them changes nothing
         from .boundary import scale_in_place
-        scale_in_place(self.grad, _native.SCALE_DIVIDE, scale)
+        scale_in_place(self._grad, _native.SCALE_DIVIDE, scale)
 
     @torch.no_grad()
     def scale_grads(self, factor: float) -> None:
@@ -869,7 +1031,10 @@ class FlatParamGroup:
             return
         from .boundary import scale_in_place
         scale_in_place(target, _native.SCALE_MULTIPLY, factor)
-        self._grad_dirty = True
+        if target is self.grad_shard:
+            self._shard_dirty = True
+        else:
+            self._grad_dirty = True
 
     @property
     def shard(self) -> torch.Tensor:
@@ -898,8 +1063,9 @@ def build_flat_groups(
 ) -> Tuple[List[FlatParamGroup], List[dict]]:
     """torch-style group dicts -> FlatParamGroups + option dicts
     (flat.py:263-291).  The groups' masters and moments are placed together
-    by ``state_buffers`` (one arena of ``state_spacing``-byte windows, or
-    separate allocations when it is 0)."""
+    by ``place_state`` (one arena of ``state_spacing``-byte windows, or
+    separate allocations when it is 0); every group records the result in
+    ``state_placement``."""
     device = torch.device(device)
     kept: List[Tuple[List[nn.Parameter], dict]] = []
     for group in param_groups:
@@ -912,10 +1078,12 @@ def build_flat_groups(
     sizes = [state_sizes(FlatLayout([p.numel() for p in params], rank=rank, world_size=world_size,
                                     zero_stage=zero_stage), zero_stage)
              for params, _ in kept]
-    states = state_buffers(sizes, device, state_spacing)
+    states, placement = place_state(sizes, device, state_spacing)
     flat_groups = [
         FlatParamGroup(params, rank=rank, world_size=world_size, zero_stage=zero_stage, device=device,
                        state=state)
         for (params, _), state in zip(kept, states)
     ]
+    for g in flat_groups:
+        g.state_placement = placement
     return flat_groups, [opts for _, opts in kept]

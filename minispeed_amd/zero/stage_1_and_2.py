@@ -78,6 +78,7 @@ class ZeROOptimizer:
         for g in self.flat_groups:
             if self.zero_stage >= 2:
                 comm.reduce_scatter(g.grad_shard, g.grad)
+                g._shard_dirty = True
             else:
                 comm.all_reduce(g.grad)
 

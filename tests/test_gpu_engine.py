@@ -393,7 +393,7 @@ def test_thousands_of_tiny_tensors_against_the_oracle():
     rows, most tiles straddling segment edges), fp16, ZeRO-2, clip: every
     boundary against the oracle started from the GPU's own state."""
     from oracle import boundary as ob
-    from tests.helpers import clip_override, master_step_within_ulps
+    from tests.helpers import clip_override, master_step_within_ulps, step_hyper
 
     rng = np.random.default_rng(5)
     sizes = rng.integers(1, 301, size=3000)
@@ -423,11 +423,13 @@ def test_thousands_of_tiny_tensors_against_the_oracle():
             rp.grad = gr.clone()
         engine.micro_steps += 1
         ref.micro_steps += 1
+        hp = step_hyper(engine)
         assert engine.step() is True and ref.step(clip_override=clip_override(engine)) is True
         assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
-        ok, worst = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
-                                            ref.groups[0].data.numpy(), 2.0)
-        assert ok, (step, worst)
+        ok, worst, nsq = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
+                                                 ref.groups[0].data.numpy(), st["exp_avg"].cpu().numpy(),
+                                                 st["exp_avg_sq"].cpu().numpy(), **hp)
+        assert ok, (step, worst, nsq)
         assert torch.equal(st["exp_avg"].cpu(), ref.state[0]["exp_avg"])
         assert torch.equal(st["exp_avg_sq"].cpu(), ref.state[0]["exp_avg_sq"])
         master = g.data.cpu()
@@ -473,36 +475,58 @@ def test_zero_size_parameter_in_the_list(stage):
 
 
 def test_state_arena_windows():
-    """With a window the buffers are zeroed views of one allocation of three
-    windows: array j of every group at window j, the groups back to back at
-    the same offsets (2 MiB aligned); a column larger than a window, or no
-    window, gives separate allocations."""
-    from minispeed_amd.flat import state_buffers
+    """With a window the buffers lie in one allocation of three windows:
+    array j of every group at window j, the groups back to back at the same
+    offsets (2 MiB slots), zeroed.  The arena is carved through torch's
+    caching allocator: the buffers hold only their slots, and the windows'
+    unused part is free memory of the allocator that later tensors are
+    served from.  A column larger than a window, or no window, gives
+    separate allocations."""
+    from minispeed_amd.flat import place_state
 
     dev = torch.device(DEV)
     mib = 1 << 20
-    win = 8 * mib
+    win = 512 * mib
     sizes = [[1000, 700, 700], [mib // 4 + 3, mib // 4 + 3, 5]]
     torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    def large_reserved():
+        return torch.cuda.memory_stats(dev)["reserved_bytes.large_pool.current"]
+
     before = torch.cuda.memory_allocated(dev)
-    bufs = state_buffers(sizes, dev, win)
+    reserved = large_reserved()
+    bufs, placement = place_state(sizes, dev, win)
     torch.cuda.synchronize()
     assert [[b.numel() for b in row] for row in bufs] == sizes
     flat_bufs = [b for row in bufs for b in row]
     assert all(b.dtype == torch.float32 and b.is_contiguous() and int(b.count_nonzero()) == 0
                for b in flat_bufs)
     base = bufs[0][0].data_ptr()
-    assert all(b.untyped_storage().data_ptr() == base for b in flat_bufs)
     for j in range(3):
         assert bufs[0][j].data_ptr() - base == j * win
         assert bufs[1][j].data_ptr() - base == j * win + 2 * mib     # after group 0's 2 MiB slot
-    assert torch.cuda.memory_allocated(dev) - before == 3 * win
+    assert placement.window == win and placement.arena_bytes == 3 * win
+    assert placement.held_bytes == 6 * 2 * mib
+    assert placement.returned_bytes == 3 * win - 12 * mib
+    # the state holds its slots only; the arena is one new segment of 3 windows
+    assert torch.cuda.memory_allocated(dev) - before == 12 * mib
+    assert large_reserved() - reserved == 3 * win
+    # tensors allocated afterwards are served from the windows' gaps: no new segment
+    later = [torch.empty(400 * mib, dtype=torch.uint8, device=dev) for _ in range(3)]
+    assert all(base <= t.data_ptr() and t.data_ptr() + t.numel() <= base + 3 * win for t in later)
+    assert large_reserved() - reserved == 3 * win
+    for t in later:
+        t.fill_(0xFF)
+    torch.cuda.synchronize()
+    assert all(int(b.count_nonzero()) == 0 for b in flat_bufs)
     bufs[1][1].fill_(1.0)
     assert all(int(b.count_nonzero()) == 0 for b in flat_bufs if b is not bufs[1][1])
-    big = state_buffers([[3 * mib, 10, 10]], dev, win)[0]              # 12 MiB > 8 MiB window
-    assert len({b.untyped_storage().data_ptr() for b in big}) == 3
-    plain = state_buffers([[1000, 1000, 1000]], dev, 0)[0]
-    assert len({b.untyped_storage().data_ptr() for b in plain}) == 3
+    del later
+    big, big_place = place_state([[300 * mib, 10, 10]], dev, win)    # 1200 MiB > 512 MiB window
+    assert len({b.untyped_storage().data_ptr() for b in big[0]}) == 3 and big_place.window == 0
+    plain, plain_place = place_state([[1000, 1000, 1000]], dev, 0)
+    assert len({b.untyped_storage().data_ptr() for b in plain[0]}) == 3
+    assert plain_place.arena_bytes == 0 and plain_place.returned_bytes == 0
 
 
 def test_two_groups_share_one_arena():
@@ -516,12 +540,12 @@ def test_two_groups_share_one_arena():
                            config=cfg)
     g0, g1 = engine.flat_groups
     st0, st1 = engine.optimizer.state
-    base = g0.data.untyped_storage().data_ptr()
-    for t in (g0.data, g1.data, st0["exp_avg"], st1["exp_avg"], st0["exp_avg_sq"], st1["exp_avg_sq"]):
-        assert t.untyped_storage().data_ptr() == base
     win = st0["exp_avg"].data_ptr() - g0.data.data_ptr()
-    assert win > 0 and st0["exp_avg_sq"].data_ptr() - st0["exp_avg"].data_ptr() == win
+    assert win == engine.state_placement.window > 0
+    assert st0["exp_avg_sq"].data_ptr() - st0["exp_avg"].data_ptr() == win
     assert st1["exp_avg"].data_ptr() - g1.data.data_ptr() == win
+    assert g1.data.data_ptr() - g0.data.data_ptr() == 2 << 20
+    assert g0.state_placement is g1.state_placement is engine.state_placement
 
 
 @pytest.mark.parametrize("stage", [1, 3])
