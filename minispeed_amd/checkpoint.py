@@ -85,13 +85,26 @@ def _full_parameters(engine, refresh: bool = False) -> Iterator[None]:
     opt = engine.optimizer
     gathered_before = opt.params_gathered
     opt.gather_parameters()
-    yield
-    if refresh and engine.config.zero_stage >= 3:
-        opt.free_parameters()
-        if gathered_before:
-            opt.gather_parameters()
-    elif not gathered_before:
-        opt.free_parameters()
+    ok = False
+    try:
+        yield
+        ok = True
+    finally:
+        # also when the block raised (a missing shard, a size mismatch, a
+        # disk error): the ZeRO-3 placeholders come back, and after a failed
+        # load the parameters (which the module's load_state_dict may already
+        # have overwritten) are recast from the masters, which a failed load
+        # leaves untouched
+        if refresh and engine.config.zero_stage >= 3:
+            opt.free_parameters()
+            if gathered_before:
+                opt.gather_parameters()
+        else:
+            if refresh and not ok:
+                for g in engine.flat_groups:
+                    g.copy_flat_to_model()
+            if not gathered_before:
+                opt.free_parameters()
 
 
 def _shard_payload(engine) -> dict:
@@ -110,9 +123,10 @@ def _restore_masters(engine, saved) -> None:
     groups = engine.flat_groups
     if len(saved) != len(groups):
         raise RuntimeError(f"checkpoint has {len(saved)} parameter groups, the engine {len(groups)}")
-    for g, buf in zip(groups, saved):
+    for g, buf in zip(groups, saved):      # every group checked before any is written
         if buf.numel() != g.data.numel():
             raise RuntimeError(f"master buffer of {buf.numel()} elements, expected {g.data.numel()}")
+    for g, buf in zip(groups, saved):
         g.data.copy_(buf)
         g.copy_flat_to_model()
 

@@ -24,6 +24,15 @@ read a second time: the boundary moves 30 B/param (K3) instead of 34.
 When the loss scale that unscaled the statistics is not the boundary's
 (it changed inside the window), the boundary scans the sums again.
 
+K5's tiles are 2048-element pieces of each parameter's slice, K1's are
+2048-element pieces of the flat space; where a parameter does not start on
+a multiple of 2048 the two tilings group the elements differently, so the
+fp64 partial sums are added in another order and the norm (with it the clip
+coefficient, and the masters where clipping applies) can differ from a K1
+scan of the same sums in the last bit of the fp32 norm.  Both orders are
+fixed: each path is run-to-run deterministic, and the tests hold the two
+within 1.2e-7 relative of each other and within 1e-5 of the oracle.
+
 Differences from minispeed, which is why the mode is off by default:
 
 * sums are rounded to fp32 after each micro-batch instead of to the

@@ -19,21 +19,29 @@ from . import comm
 
 class Timer:
     """Accumulated seconds of one named section; ``with timer.section():``
-    (or ``with timer:``) adds the wall time of the block."""
+    (or ``with timer:``) adds the wall time of the block.  ``started_at``
+    (minispeed/utils.py:18) is the ``time.perf_counter()`` value at which
+    the outermost open section began, None while none is open."""
 
-    __slots__ = ("name", "elapsed", "_open")
+    __slots__ = ("name", "elapsed", "started_at", "_open")
 
     def __init__(self, name: str):
         self.name = name
         self.elapsed = 0.0
+        self.started_at = None
         self._open: List[float] = []    # start times of the sections entered, innermost last
 
     def __enter__(self) -> "Timer":
-        self._open.append(time.perf_counter())
+        now = time.perf_counter()
+        if not self._open:
+            self.started_at = now
+        self._open.append(now)
         return self
 
     def __exit__(self, *exc) -> bool:
         self.elapsed += time.perf_counter() - self._open.pop()
+        if not self._open:
+            self.started_at = None
         return False
 
     def section(self) -> "Timer":

@@ -8,14 +8,19 @@ placeholders refreshed from the masters (stage_3.py:88-100).
 
 The placeholders are views into one model-dtype buffer of the shard
 (``FlatParamGroup.model_shard``), and at world size 1 the gathered
-parameters are shaped views into the same buffer: the gather is a change of
-views, and the cast runs only when the buffer does not already hold the cast
-of the current masters (after a boundary taken without a gather, a
-standalone ``step()``, or an in-place write to the masters or parameters).
-In the fused boundary K3 writes the cast of the updated masters straight
-into the buffer, which is what the reference's Adam step followed by
-``free_parameters`` leaves behind.  On a skipped step the masters are
-unchanged and the buffer is refreshed by the cast kernel instead.
+parameters are shaped views into the same buffer, so neither gather nor
+free allocates.  The gather casts the masters into that buffer (K4) every
+time, as the reference's gather does, so whatever was written into a freed
+placeholder is overwritten.  With ``gather_reuse`` (the
+``hip_boundary.stage3_gather_reuse`` option) the cast is skipped when the
+buffer already holds the cast of the current masters by the version
+counters of the masters and the parameters (``model_is_fresh``); writes
+through a freed placeholder's ``.data`` are not seen by those counters and
+then survive the gather.  In the fused boundary K3 writes the cast of the
+updated masters straight into the buffer, which is what the reference's
+Adam step followed by ``free_parameters`` leaves behind.  On a skipped step
+the masters are unchanged and the buffer is refreshed by the cast kernel
+instead.
 """
 
 from __future__ import annotations
@@ -35,6 +40,8 @@ class ZeROStage3Optimizer(ZeROOptimizer):
         self._gathered = False
         # placeholders created for the current boundary (K3 writes them)
         self._boundary_freed = False
+        # skip the gather's cast when the buffer is fresh (opt-in)
+        self.gather_reuse = False
 
     @property
     def params_gathered(self) -> bool:
@@ -51,7 +58,7 @@ class ZeROStage3Optimizer(ZeROOptimizer):
                     f"(shard {g.numel_shard()} of {g.numel_padded})"
                 )
             g.materialize_params()
-            if not g.model_is_fresh():
+            if not (self.gather_reuse and g.model_is_fresh()):
                 g.copy_flat_to_model()
         self._gathered = True
 
@@ -105,5 +112,5 @@ class ZeROStage3Optimizer(ZeROOptimizer):
             for g in self.flat_groups:
                 g.masters_written()       # placeholders keep the old values
         for g in self.flat_groups:
-            if g.grad is not None:
+            if g._grad is not None:
                 g.grad = None  # the full flat grad never outlives the boundary

@@ -152,19 +152,57 @@ def k4(table: Table, mdtype, flat: torch.Tensor, begin, end):
 __all__ = [name for name in dir() if not name.startswith("_")] + ["adamw_params"]
 
 
-def master_step_within_ulps(before, got, want, ulps=2.0):
-    """Per-step master check: |got - want| <= ulps * spacing of the largest
-    operand of the final addition p + u (p_before, the update u = want -
-    before, and the result).  Returns (ok, worst ratio)."""
-    before = np.asarray(before, dtype=np.float32)
-    got = np.asarray(got, dtype=np.float32)
-    want = np.asarray(want, dtype=np.float32)
-    upd = np.abs(want.astype(np.float64) - before.astype(np.float64)).astype(np.float32)
-    scale = np.maximum(np.maximum(np.abs(before), np.abs(want)), upd)
+def master_step_within_ulps(before, got, want, m, v, *, lr, betas, eps, wd, step, ulps=2.0):
+    """Per-step master check of the GPU (``got``) against the oracle
+    (``want``), both started from ``before``, with ``m`` / ``v`` the step's
+    new moments (equal on both sides, bit for bit; the callers assert that)
+    and the step's hyper-parameters.
+
+    The last part of the update, p + (-lr * (m / bc1)) / (sqrt(v / bc2) +
+    eps) after the decay, is recomputed from the moments twice: with CPU
+    torch's sqrt, which must give the oracle's masters bit for bit, and with
+    a correctly rounded sqrt, which must give the GPU's bit for bit.  Then
+    |got - want| <= ulps * spacing(want) per element, except where torch's
+    sqrt is not correctly rounded (about 0.6% of its inputs): there the two
+    updates differ by construction, and the GPU is the exactly rounded one.
+    Returns (ok, worst ratio to spacing(want) over the elements whose sqrt
+    agrees, number of elements over the bound whose sqrt differs)."""
+    from oracle import recipe
+
+    f = np.float32
+    b1, b2 = float(betas[0]), float(betas[1])
+    before = np.asarray(before, dtype=f)
+    got = np.asarray(got, dtype=f)
+    want = np.asarray(want, dtype=f)
+    m = np.asarray(m, dtype=f)
+    v = np.asarray(v, dtype=f)
+    p1 = recipe.fma32(before, f(-lr * wd), before) if wd != 0.0 else before
+    q = v / f(1.0 - b2 ** step)
+    den_cpu = torch.from_numpy(q.copy()).sqrt().numpy() + f(eps)   # the oracle's sqrt
+    den_rn = np.sqrt(q) + f(eps)
+    num = f(-lr) * (m / f(1.0 - b1 ** step))
+    if not np.array_equal((p1 + num / den_cpu).view(np.int32), want.view(np.int32)):
+        return False, float("inf"), -1          # the oracle is not this update
+    if not np.array_equal((p1 + num / den_rn).view(np.int32), got.view(np.int32)):
+        return False, float("inf"), -2          # the GPU is not the exactly rounded update
     diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    ratio = diff / np.spacing(scale).astype(np.float64)
-    worst = float(ratio.max()) if ratio.size else 0.0
-    return worst <= ulps, worst
+    ratio = diff / np.spacing(np.abs(want)).astype(np.float64)
+    sqrt_differs = den_cpu != den_rn
+    over = ratio > ulps
+    if np.any(over & ~sqrt_differs):
+        return False, float(ratio[~sqrt_differs].max()), int(np.sum(over & sqrt_differs))
+    worst = float(ratio[~sqrt_differs].max()) if np.any(~sqrt_differs) else 0.0
+    return True, worst, int(np.sum(over))
+
+
+def step_hyper(engine, gi: int = 0) -> dict:
+    """Group ``gi``'s AdamW hyper-parameters for the step about to run (read
+    before ``engine.step()``: the scheduler moves lr afterwards) and the
+    step count that step will use."""
+    from minispeed_amd.optim.adam import FlatAdam
+
+    lr, betas, eps, wd = FlatAdam.hyper(engine.optimizer.param_groups[gi])
+    return dict(lr=lr, betas=betas, eps=eps, wd=wd, step=int(engine.optimizer.state[gi]["step"]) + 1)
 
 
 def clip_override(engine):

@@ -47,10 +47,50 @@ def _fake_engine(world_size=1, rank=0, ngroups=1, numel=696):
               for s in [(7, 5), (3,), (16, 33), (1,), (129,)]]
     opt = SimpleNamespace(params_gathered=True, gather_parameters=lambda: None,
                           free_parameters=lambda: None)
-    groups = [SimpleNamespace(data=torch.zeros(numel)) for _ in range(ngroups)]
+    groups = [SimpleNamespace(data=torch.zeros(numel), copy_flat_to_model=lambda: None)
+              for _ in range(ngroups)]
     return SimpleNamespace(rank=rank, world_size=world_size, module=Holder(params),
                            optimizer=opt, flat_groups=groups,
                            config=SimpleNamespace(zero_stage=2))
+
+
+class _TrackingOptimizer:
+    """Stands in for a ZeRO-3 optimizer: records gathers, frees and the
+    parameters' state, so a failed load can be checked for what it leaves."""
+
+    def __init__(self, gathered):
+        self.params_gathered = gathered
+        self.calls = []
+
+    def gather_parameters(self):
+        self.calls.append("gather")
+        self.params_gathered = True
+
+    def free_parameters(self):
+        self.calls.append("free")
+        self.params_gathered = False
+
+
+@pytest.mark.parametrize("stage", [2, 3])
+@pytest.mark.parametrize("gathered", [False, True])
+def test_failed_load_restores_the_parameters(stage, gathered):
+    """A load that raises half-way (here: the rank's optimizer shard is
+    missing, after the module's weights were loaded) leaves the ZeRO-3
+    gather state as it found it and the parameters recast from the
+    untouched masters."""
+    eng = _fake_engine(rank=1)
+    eng.config.zero_stage = stage
+    eng.optimizer = _TrackingOptimizer(gathered)
+    casts = []
+    for g in eng.flat_groups:
+        g.copy_flat_to_model = lambda g=g: casts.append(g)
+    with pytest.raises(FileNotFoundError, match="rank 1"):
+        ckpt.load_checkpoint(eng, checkpoint_root("fp16_z2_clip"))
+    assert eng.optimizer.params_gathered is gathered
+    if stage >= 3:
+        assert "free" in eng.optimizer.calls          # placeholders refreshed from the masters
+    else:
+        assert casts == eng.flat_groups
 
 
 def test_load_refuses_another_world_size():

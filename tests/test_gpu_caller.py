@@ -40,7 +40,7 @@ from torch import nn
 import minispeed_amd as ms
 from oracle import boundary as ob
 from tests.golden_cases import DTYPES, META, MLP, arrays, scheduler_params
-from tests.helpers import clip_override, master_step_within_ulps
+from tests.helpers import clip_override, master_step_within_ulps, step_hyper
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -132,6 +132,7 @@ def test_backward_and_gating_replay_minispeeds_trace(name):
             for rp, p in zip(ref_params, params):
                 rp.grad = p.grad.detach().cpu().clone()
             ref.micro_steps = engine.micro_steps
+            hp = step_hyper(engine)
             applied = engine.step()
             assert engine.step() is False                # one update per boundary
             assert ref.step(clip_override=clip_override(engine) if applied else None) == applied
@@ -145,9 +146,10 @@ def test_backward_and_gating_replay_minispeeds_trace(name):
                                               ref.state[0]["exp_avg"].numpy())
                 np.testing.assert_array_equal(st["exp_avg_sq"].cpu().numpy(),
                                               ref.state[0]["exp_avg_sq"].numpy())
-                ok, worst = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
-                                                    ref.groups[0].data.numpy(), 2.0)
-                assert ok, (s, worst)
+                ok, worst, nsq = master_step_within_ulps(
+                    before.numpy(), g.data.cpu().numpy(), ref.groups[0].data.numpy(),
+                    st["exp_avg"].cpu().numpy(), st["exp_avg_sq"].cpu().numpy(), **hp)
+                assert ok, (s, worst, nsq)
             else:
                 assert torch.equal(g.data.cpu(), before)
             boundaries.append({"applied": bool(applied), "scale": sc.scale,

@@ -31,7 +31,7 @@ from torch import nn
 import minispeed_amd as ms
 from minispeed_amd import _native
 from oracle import boundary as ob
-from tests.helpers import clip_override, master_step_within_ulps
+from tests.helpers import clip_override, master_step_within_ulps, step_hyper
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -379,12 +379,14 @@ def test_matches_the_oracle_given_the_fp32_sums(dtype):
                        engine.lr_scheduler.last_epoch,
                        [pg["lr"] for pg in engine.optimizer.param_groups])
         ref.micro_steps += 3
+        hp = step_hyper(engine)
         assert engine.step() is True
         assert ref.step(flat_grads=[flat], clip_override=clip_override(engine)) is True
         assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
-        ok, worst = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
-                                            ref.groups[0].data.numpy(), 2.0)
-        assert ok, (w, worst)
+        ok, worst, nsq = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
+                                                 ref.groups[0].data.numpy(), st["exp_avg"].cpu().numpy(),
+                                                 st["exp_avg_sq"].cpu().numpy(), **hp)
+        assert ok, (w, worst, nsq)
         assert torch.equal(st["exp_avg"].cpu(), ref.state[0]["exp_avg"])
         assert torch.equal(st["exp_avg_sq"].cpu(), ref.state[0]["exp_avg_sq"])
         # the fp32 sums are not half values: half accumulation would differ

@@ -29,7 +29,7 @@ import minispeed_amd as ms
 from minispeed_amd.workloads import shapes_of
 from oracle import boundary as ob
 from oracle import recipe
-from tests.helpers import clip_override, master_step_within_ulps, relative_within
+from tests.helpers import clip_override, master_step_within_ulps, relative_within, step_hyper
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -58,6 +58,28 @@ def _engine(shapes, cfg, seed=0):
     params = _params(shapes, seed)
     mod = nn.ParameterList(params)
     return ms.initialize(model=mod, model_parameters=list(mod), config=cfg), params
+
+
+class _Sample:
+    """``count`` seeded flat indices of a group (unique, sorted) and the
+    values of a ragged tensor list (gradients, parameters) there."""
+
+    def __init__(self, g, count, seed):
+        rng = np.random.default_rng(seed)
+        offsets = np.array(g.layout.offsets, dtype=np.int64)
+        self.idx = np.unique(rng.integers(0, g.numel, size=count))
+        self.pi = np.searchsorted(offsets, self.idx, side="right") - 1
+        self.local = self.idx - offsets[self.pi]
+        self.idx_t = torch.from_numpy(self.idx).to(DEV)
+
+    def gather(self, tensors, dtype=np.float32):
+        """flat values of a ragged list at the sampled indices, on the CPU"""
+        out = np.empty(len(self.idx), dtype=dtype)
+        for k in np.unique(self.pi):
+            sel = np.nonzero(self.pi == k)[0]
+            t = tensors[k].detach().reshape(-1)[torch.from_numpy(self.local[sel]).to(DEV)].cpu()
+            out[sel] = t.float().numpy() if dtype == np.float32 else t.view(torch.int16).numpy()
+        return out
 
 
 def _grads(shapes, dtype, gen, scale=1.0, std=1e-3):
@@ -90,6 +112,7 @@ def test_gpt2_small_fp16_zero2_against_oracle():
             rp.grad = gr.cpu()
         engine.micro_steps += 1
         ref.micro_steps += 1
+        hp = step_hyper(engine)
         assert engine.step() is True
         # per-step checks run the oracle's AdamW on the GPU's clip coefficient;
         # afterwards the oracle runs on its own (its own norms and coefficients)
@@ -99,8 +122,13 @@ def test_gpt2_small_fp16_zero2_against_oracle():
         if step < checked:
             got = g.data.detach().cpu().numpy()
             want = ref.groups[0].data.numpy()
-            ok, worst = master_step_within_ulps(before.numpy(), got, want, 2.0)
-            assert ok, (step, worst)
+            ok, worst, nsq = master_step_within_ulps(
+                before.numpy(), got, want, engine.optimizer.state[0]["exp_avg"].cpu().numpy(),
+                engine.optimizer.state[0]["exp_avg_sq"].cpu().numpy(), **hp)
+            print(f"[gpt2-124m] step {step}: masters within {worst:.2f} ulp of the oracle's; "
+                  f"{nsq} elements further off where torch's CPU sqrt is not correctly rounded",
+                  flush=True)
+            assert ok, (step, worst, nsq)
             np.testing.assert_array_equal(engine.optimizer.state[0]["exp_avg"].cpu().numpy(),
                                           ref.state[0]["exp_avg"].numpy())
             np.testing.assert_array_equal(engine.optimizer.state[0]["exp_avg_sq"].cpu().numpy(),
@@ -135,6 +163,11 @@ def test_overflow_stress_350m_trajectory():
     g = engine.flat_groups[0]
     specials = [float("inf"), float("-inf"), float("nan")]
     skipped = 0
+    # applied steps checked bit for bit against the kernels' recipe on 2^18
+    # sampled elements: the first ones, the ones right after an injected
+    # overflow (the scale just halved), and the last ones (scale 1)
+    checked = {0, 1, 4, 8, 100, 196, 197, 198}
+    sample = _Sample(g, 1 << 18, seed=5)
     for step in range(200):
         grads = _grads(shapes, torch.float16, gen, scale=engine.loss_scaler.scale)
         inject = step % 4 == 3
@@ -144,10 +177,31 @@ def test_overflow_stress_350m_trajectory():
                 grads[ti].view(-1)[int(rng.integers(0, sizes[ti]))] = specials[int(rng.integers(0, 3))]
             state0 = (g.data.clone(), engine.optimizer.state[0]["exp_avg"].clone(),
                       engine.optimizer.state[0]["exp_avg_sq"].clone(), params[5].detach().clone())
+        if step in checked:
+            assert not inject
+            it = sample.idx_t
+            p0, m0, v0 = (x[it].cpu().numpy() for x in (g.data, engine.optimizer.state[0]["exp_avg"],
+                                                       engine.optimizer.state[0]["exp_avg_sq"]))
+            g_s = sample.gather(grads)
+            lr = engine.optimizer.param_groups[0]["lr"]
+            t_adam = engine.optimizer.state[0]["step"] + 1
+            scale_before = engine.loss_scaler.scale
         for p, gr in zip(params, grads):
             p.grad = gr
         engine.micro_steps += 1
         applied = engine.step()
+        if step in checked:
+            sc = engine.last_boundary
+            wp, wm, wv = recipe.adamw_step(p0, m0, v0, g_s, lr=lr, betas=(0.9, 0.999), eps=1e-8,
+                                           wd=0.01, step=t_adam, grad_scale=scale_before,
+                                           unscale=scale_before != 1.0,
+                                           clip_coef=float(np.float32(sc.coef)) if sc.clip_applied else None)
+            for got, want in ((g.data, wp), (engine.optimizer.state[0]["exp_avg"], wm),
+                              (engine.optimizer.state[0]["exp_avg_sq"], wv)):
+                np.testing.assert_array_equal(got[it].cpu().numpy().view(np.int32), want.view(np.int32),
+                                              err_msg=str(step))
+            np.testing.assert_array_equal(sample.gather(params, np.int16),
+                                          torch.from_numpy(wp).half().view(torch.int16).numpy())
         scaler.update(overflow=inject)
         skipped += inject
         assert applied == (not inject), step
@@ -182,22 +236,8 @@ def test_1p3b_bf16_gas4_norm_sampled_elements_and_modes():
                                                   "warmup_num_steps": 100, "total_num_steps": 1000}}
     engine, params = _engine(shapes, _cfg("bf16", 1, sched=sched, gas=4), seed=3)
     g = engine.flat_groups[0]
-    n = g.numel
-    offsets = np.array(g.layout.offsets, dtype=np.int64)
-    rng = np.random.default_rng(0)
-    idx = np.unique(rng.integers(0, n, size=1_000_000))
-    pi = np.searchsorted(offsets, idx, side="right") - 1
-    local = idx - offsets[pi]
-    idx_t = torch.from_numpy(idx).to(DEV)
-
-    def gather(tensors):
-        """flat values of a ragged list at the sampled indices, on the CPU"""
-        out = np.empty(len(idx), dtype=np.float32)
-        for k in np.unique(pi):
-            sel = np.nonzero(pi == k)[0]
-            t = tensors[k].detach().reshape(-1)
-            out[sel] = t[torch.from_numpy(local[sel]).to(DEV)].float().cpu().numpy()
-        return out
+    sample = _Sample(g, 1_000_000, seed=0)
+    idx, idx_t, gather = sample.idx, sample.idx_t, sample.gather
 
     for step in range(2):
         grads = _bf16_gas4_grads(shapes, seed=10 + step)

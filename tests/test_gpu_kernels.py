@@ -261,8 +261,9 @@ def test_k3_against_torch_restatement(gdtype):
     ob.adam_update(tp, tg, tm, tv, lr, betas, eps, wd, step)
     np.testing.assert_array_equal(dm.cpu().numpy(), tm.numpy())
     np.testing.assert_array_equal(dv.cpu().numpy(), tv.numpy())
-    ok, worst = master_step_within_ulps(p, dp.cpu().numpy(), tp.numpy())
-    assert ok, worst
+    ok, worst, nsq = master_step_within_ulps(p, dp.cpu().numpy(), tp.numpy(), tm.numpy(), tv.numpy(),
+                                             lr=lr, betas=betas, eps=eps, wd=wd, step=step)
+    assert ok, (worst, nsq)
 
 
 def test_k3_skips_everything_on_overflow():

@@ -36,7 +36,7 @@ from minispeed_amd import _native
 from oracle import boundary as ob
 from oracle import recipe
 from tests.helpers import (DEV, Table, adamw_params, bits, clip_override, k1, k3, k4, layout_for,
-                           master_step_within_ulps, scalars_device, store)
+                           master_step_within_ulps, scalars_device, step_hyper, store)
 
 pytestmark = pytest.mark.gpu
 
@@ -254,11 +254,13 @@ def test_engine_on_a_shifted_list_against_the_oracle(dtype, stage):
             rp.grad = gr.clone()
         engine.micro_steps += 1
         ref.micro_steps += 1
+        hp = step_hyper(engine)
         assert engine.step() is True and ref.step(clip_override=clip_override(engine)) is True
         assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
-        ok, worst = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
-                                            ref.groups[0].data.numpy(), 2.0)
-        assert ok, (step, worst)
+        ok, worst, nsq = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
+                                                 ref.groups[0].data.numpy(), st["exp_avg"].cpu().numpy(),
+                                                 st["exp_avg_sq"].cpu().numpy(), **hp)
+        assert ok, (step, worst, nsq)
         assert torch.equal(st["exp_avg"].cpu(), ref.state[0]["exp_avg"])
         assert torch.equal(st["exp_avg_sq"].cpu(), ref.state[0]["exp_avg_sq"])
     master = g.data.cpu()

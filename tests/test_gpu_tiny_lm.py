@@ -35,7 +35,7 @@ from minispeed_amd.workloads import numel, shapes_of
 from oracle import boundary as ob
 from tests import tinylm
 from tests.golden_cases import META
-from tests.helpers import clip_override, master_step_within_ulps
+from tests.helpers import clip_override, master_step_within_ulps, step_hyper
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -71,12 +71,14 @@ def test_tiny_lm_trains_through_the_engine_and_matches_the_oracle_and_minispeed(
         for rp, gr in zip(ref_params, grads):
             rp.grad = gr
         ref.micro_steps += 1
+        hp = step_hyper(engine)
         assert engine.step() is True and ref.step(clip_override=clip_override(engine)) is True
         norms.append(engine.grad_norm)
         assert abs(engine.grad_norm - ref.grad_norm) <= 1e-5 * ref.grad_norm
-        ok, worst = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
-                                            ref.groups[0].data.numpy(), 2.0)
-        assert ok, (step, worst)
+        ok, worst, nsq = master_step_within_ulps(before.numpy(), g.data.cpu().numpy(),
+                                                 ref.groups[0].data.numpy(), st["exp_avg"].cpu().numpy(),
+                                                 st["exp_avg_sq"].cpu().numpy(), **hp)
+        assert ok, (step, worst, nsq)
         np.testing.assert_array_equal(st["exp_avg"].cpu().numpy(), ref.state[0]["exp_avg"].numpy())
         np.testing.assert_array_equal(st["exp_avg_sq"].cpu().numpy(), ref.state[0]["exp_avg_sq"].numpy())
         # fp32 model: the parameters are the masters

@@ -1,13 +1,16 @@
 """ZeRO-3 gather/free as views of one model-dtype buffer (world size 1).
 
 The freed placeholders and the gathered parameters are views into
-``FlatParamGroup.model_shard``: gather and free allocate nothing, the gather
-runs no cast when the buffer already holds the cast of the masters, and the
+``FlatParamGroup.model_shard``: gather and free allocate nothing, and the
 gathered parameters always equal the reference's cast-on-gather of the
 current masters (stage_3.py:67-86), bit for bit, whatever happened since the
 last cast: a boundary with or without a gather, a skipped boundary, a
 standalone optimizer step, in-place writes to the masters or the
-parameters, a checkpoint load.
+parameters, a checkpoint load, a write through a freed placeholder's
+``.data``.  By default every gather casts, as the reference's does; with
+``hip_boundary.stage3_gather_reuse`` the gather runs no cast when the buffer
+already holds the cast of the masters by the version counters, and a write
+through a placeholder's ``.data`` (which they do not see) survives it.
 """
 
 from __future__ import annotations
@@ -33,13 +36,13 @@ class MLP(nn.Module):
         return self.net(x)
 
 
-def _engine(dtype="fp16"):
+def _engine(dtype="fp16", reuse=False):
     torch.manual_seed(0)
     model = MLP().to(DEV)
     cfg = {"train_micro_batch_size_per_gpu": 4, "gradient_accumulation_steps": 1,
            "gradient_clipping": 1.0, "dtype": dtype,
            "optimizer": {"type": "AdamW", "params": {"lr": 1e-2, "weight_decay": 0.01}},
-           "zero_optimization": {"stage": 3}}
+           "zero_optimization": {"stage": 3}, "hip_boundary": {"stage3_gather_reuse": reuse}}
     if dtype == "fp16":
         cfg["fp16"] = {"enabled": True, "loss_scale": 0, "initial_scale_power": 8}
     engine = ms.initialize(model=model, model_parameters=list(model.parameters()), config=cfg)
@@ -82,8 +85,10 @@ def _assert_gathered_is_cast_of_masters(engine, model):
         assert torch.equal(p.data.view(torch.int16), want.view(torch.int16))
 
 
-def test_gather_and_free_are_views_that_allocate_nothing():
-    engine, model = _engine()
+@pytest.mark.parametrize("reuse", [False, True])
+def test_gather_and_free_are_views_that_allocate_nothing(reuse):
+    engine, model = _engine(reuse=reuse)
+    assert engine.optimizer.gather_reuse is reuse
     g = engine.flat_groups[0]
     counter = CastCounter(g)
     assert _train_step(engine, 1) is True
@@ -96,7 +101,7 @@ def test_gather_and_free_are_views_that_allocate_nothing():
     before = torch.cuda.memory_allocated()
     n0 = counter.n
     engine.optimizer.gather_parameters()
-    assert counter.n == n0                                  # fresh: no cast
+    assert counter.n == n0 + (0 if reuse else 1)            # reuse: fresh, no cast
     assert torch.cuda.memory_allocated() == before
     _assert_gathered_is_cast_of_masters(engine, model)
     engine.optimizer.free_parameters()
@@ -106,7 +111,9 @@ def test_gather_and_free_are_views_that_allocate_nothing():
 @pytest.mark.parametrize("event", ["boundary_without_gather", "standalone_step", "masters_inplace",
                                    "param_inplace", "skipped_boundary", "load_state_dict"])
 def test_gather_recasts_whenever_the_copy_may_be_stale(event):
-    engine, model = _engine()
+    """With gather_reuse: the cast is skipped only while the version
+    counters show the buffer holds the cast of the current masters."""
+    engine, model = _engine(reuse=True)
     g = engine.flat_groups[0]
     for s in range(2):
         assert _train_step(engine, 10 + s) is True
@@ -149,6 +156,32 @@ def test_gather_recasts_whenever_the_copy_may_be_stale(event):
     assert _train_step(engine, 30) is True
     engine.optimizer.gather_parameters()
     _assert_gathered_is_cast_of_masters(engine, model)
+
+
+@pytest.mark.parametrize("reuse", [False, True])
+def test_write_through_a_freed_placeholder_data(reuse):
+    """A write through a freed placeholder's ``.data`` (torch's version
+    counters do not see it).  minispeed's gather builds new parameters from
+    the cast of the masters, so the write is gone (stage_3.py:67-86): the
+    default gather does the same.  With gather_reuse the write survives the
+    gather, the documented price of skipping the cast."""
+    engine, model = _engine(reuse=reuse)
+    g = engine.flat_groups[0]
+    for s in range(2):
+        assert _train_step(engine, 40 + s) is True
+    assert not engine.optimizer.params_gathered
+    first = next(model.parameters())
+    first.data.fill_(3.0)                            # no version bump
+    engine.optimizer.gather_parameters()
+    if reuse:
+        assert bool((first.data == 3.0).all())
+    else:
+        _assert_gathered_is_cast_of_masters(engine, model)
+        assert not bool((first.data == 3.0).any())
+    engine.optimizer.free_parameters()               # refreshed from the masters either way
+    engine.optimizer.gather_parameters()
+    _assert_gathered_is_cast_of_masters(engine, model)
+    assert _train_step(engine, 50) is True
 
 
 def test_views_train_like_stage0_bitwise():

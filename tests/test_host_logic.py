@@ -268,6 +268,19 @@ def test_timers_accumulate():
     assert "step:" in t.log()
     t.reset()
     assert t("step").elapsed == 0.0
+    # minispeed's Timer carries started_at (utils.py:18): None while idle,
+    # the start of the outermost open section otherwise; settable as there
+    timer = t("io")
+    assert timer.started_at is None
+    with timer.section():
+        outer = timer.started_at
+        assert outer is not None
+        with timer:
+            assert timer.started_at == outer
+        assert timer.started_at == outer
+    assert timer.started_at is None and timer.elapsed > 0.0
+    timer.started_at = 1.0
+    assert timer.started_at == 1.0
 
 
 def test_scale_transition_equals_the_oracle_scaler_on_random_runs():

@@ -172,3 +172,36 @@ def test_ulp_distance():
     assert recipe.ulp_distance(one, np.nextafter(one, np.float32(2))) == 1
     assert recipe.ulp_distance(np.float32(-0.0), np.float32(0.0)) == 0
     assert recipe.ulp_distance(np.float32(-1e-45), np.float32(1e-45)) == 2
+
+
+def test_master_step_check_accounts_for_every_element():
+    """tests/helpers.py:master_step_within_ulps, the per-step master check of
+    the GPU tests, on the CPU: the oracle's torch AdamW (CPU sqrt) as the
+    reference side, the recipe (correctly rounded sqrt) in place of the GPU.
+    It passes, and a one-ulp change of one GPU master, or the oracle run
+    with another lr, makes it fail."""
+    from tests.helpers import master_step_within_ulps
+
+    rng = np.random.default_rng(11)
+    n = 50_000
+    p = rng.normal(0, 0.02, n).astype(np.float32)
+    m = rng.normal(0, 1e-3, n).astype(np.float32)
+    v = (rng.random(n) * 1e-6 + 1e-9).astype(np.float32)
+    g = rng.normal(0, 1e-3, n).astype(np.float32)
+    hp = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, wd=0.01, step=7)
+    tp, tm, tv = (torch.from_numpy(x.copy()) for x in (p, m, v))
+    ob.adam_update(tp, torch.from_numpy(g.copy()), tm, tv, hp["lr"], hp["betas"], hp["eps"],
+                   hp["wd"], hp["step"])
+    rp, rm, rv = recipe.adamw_step(p, m, v, g, **hp)
+    assert np.array_equal(rm.view(np.int32), tm.numpy().view(np.int32))
+    assert np.array_equal(rv.view(np.int32), tv.numpy().view(np.int32))
+    ok, worst, nsq = master_step_within_ulps(p, rp, tp.numpy(), rm, rv, **hp)
+    assert ok and worst <= 2.0 and nsq >= 0, (worst, nsq)
+    # torch's sqrt differs from the correctly rounded one on some inputs
+    q = rv / np.float32(1 - 0.999 ** 7)
+    assert np.any(torch.from_numpy(q.copy()).sqrt().numpy() != np.sqrt(q))
+    bad = rp.copy()
+    k = int(np.argmax(np.abs(rp)))
+    bad[k] = np.nextafter(bad[k], np.float32(np.inf))
+    assert not master_step_within_ulps(p, bad, tp.numpy(), rm, rv, **hp)[0]
+    assert not master_step_within_ulps(p, rp, tp.numpy(), rm, rv, **dict(hp, lr=1.1e-3))[0]
