@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MS_ABI_VERSION 7
+#define MS_ABI_VERSION 8
 
 /* groups one ms_boundary_scalars_noalloc call can scan, and the tiles
  * (MS_SCAN_TILE flat indices each) of the largest one: its static scratch
@@ -110,7 +110,9 @@ typedef struct ms_step_scalars {
   float norm;             /* sqrtf(sumsq) (stage_1_and_2.py:121)            */
   float coef;             /* fp32(max_norm / (norm + 1e-6)) if clip_applied,
                              else 1 (stage_1_and_2.py:124)                  */
-  uint32_t reserved;
+  uint32_t ready;         /* 0 in K2's device output; in its host copy set
+                             to 1 after every other field is visible to the
+                             host (see ms_norm_clip)                        */
   double coef64;          /* the same coefficient before fp32 rounding      */
   double next_scale;      /* loss scale after DynamicLossScaler.update
                              (precision.py:50-62)                           */
@@ -203,10 +205,13 @@ int ms_grad_stats(const ms_segment_t* segs, int32_t nseg, int32_t grad_dtype,
  * coef64 = max_norm / (norm + 1e-6) and clip_applied = (coef64 != 1).
  * The scaler fields are the state before this boundary.
  * out [dev] receives an ms_step_scalars_t.
- * out_host [pinned host memory, optional] receives the same struct, made
- * visible to the host before the kernel completes: the caller records an
- * event after this call and reads out_host once the event has completed,
- * with no copy (the one read-back of engine.py:278-322's two syncs).
+ * out_host [pinned host memory, optional] receives the same struct with
+ * `ready` = 1, written after every other field is visible to the host: a
+ * caller that set out_host->ready to 0 before this call can poll that word
+ * and read the struct once it is 1, while later work on the stream keeps
+ * running, with no copy and no event in the stream (the one read-back of
+ * engine.py:278-322's two syncs).  Waiting for the kernel's completion
+ * (an event, a stream synchronisation) also gives the whole struct.
  */
 int ms_norm_clip(const double* block_sumsq, const uint32_t* block_flag,
                  int32_t nblk, int32_t ngroups, int32_t has_clip,

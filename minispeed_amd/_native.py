@@ -19,7 +19,7 @@ from typing import Optional
 import torch  # noqa: F401  (must precede the dlopen below, see module doc)
 
 LIB_NAME = "libminispeed_boundary.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -60,7 +60,7 @@ class StepScalars(ctypes.Structure):
         ("sumsq", ctypes.c_float),
         ("norm", ctypes.c_float),
         ("coef", ctypes.c_float),
-        ("reserved", ctypes.c_uint32),
+        ("ready", ctypes.c_uint32),
         ("coef64", ctypes.c_double),
         ("next_scale", ctypes.c_double),
         ("next_good_steps", ctypes.c_int64),
@@ -252,7 +252,6 @@ def stream_handle(device: torch.device) -> int:
 # the kernels it brackets; the elapsed time between two such events is valid
 # once the stream has been synchronised.
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
-HIP_EVENT_DISABLE_TIMING = 0x2
 _hip: Optional[ctypes.CDLL] = None
 
 
@@ -272,9 +271,9 @@ def hip_runtime() -> ctypes.CDLL:
             hip.hipEventRecord.argtypes = [_P, _P]
             hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(_F), _P, _P]
             hip.hipEventDestroy.argtypes = [_P]
-            hip.hipEventSynchronize.argtypes = [_P]
+            hip.hipStreamSynchronize.argtypes = [_P]
             for fn in (hip.hipEventCreateWithFlags, hip.hipEventRecord, hip.hipEventElapsedTime,
-                       hip.hipEventDestroy, hip.hipEventSynchronize):
+                       hip.hipEventDestroy, hip.hipStreamSynchronize):
                 fn.restype = ctypes.c_int
             _hip = hip
     return _hip

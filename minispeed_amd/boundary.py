@@ -22,6 +22,7 @@ wait for the host: the only synchronisation is the final copy of the
 from __future__ import annotations
 
 import ctypes
+import time
 from dataclasses import dataclass
 from typing import Callable, List, Optional, Sequence, Tuple
 
@@ -65,34 +66,51 @@ def adamw_params(
     )
 
 
-class HostWait:
-    """The host's wait for K2: an event recorded on the stream right after
-    K2, without the system-scope release a default event performs (K2 makes
-    its write to pinned host memory visible before it ends, with a
-    system-scope fence of its own) and without a timestamp.  A default event
-    there costs the next kernel a cache write-back: a 5.5 us gap between K2
-    and K3."""
+class HostReadback:
+    """K2's result in pinned host memory, read without a copy and without
+    anything between K2 and K3 in the stream.
 
-    def __init__(self, device: torch.device):
-        self._hip = _native.hip_runtime()
-        ev = ctypes.c_void_p()
-        with torch.cuda.device(device):     # an event belongs to the device current at creation
-            _native.hip_check(self._hip.hipEventCreateWithFlags(
-                ctypes.byref(ev),
-                _native.HIP_EVENT_DISABLE_SYSTEM_FENCE | _native.HIP_EVENT_DISABLE_TIMING),
-                "hipEventCreateWithFlags")
-        self._ev = ev.value
+    ``arm()`` clears the struct's ``ready`` word before K2 is launched with
+    ``ptr`` as its host output; K2 writes the struct, makes it visible
+    system-wide and then sets ``ready``; ``wait()`` polls that word (K3, queued
+    behind K2, keeps running) and returns the struct.  An event recorded
+    after K2 for the host to wait on put a 4-5.5 us gap between K2 and K3.
+    If the word does not turn within ``patience`` seconds (a deep queue of
+    earlier work), the stream is synchronised instead, which also reports a
+    device error."""
 
-    def record(self, stream: int) -> None:
-        _native.hip_check(self._hip.hipEventRecord(self._ev, stream), "hipEventRecord")
+    _READY = _native.StepScalars.ready.offset
 
-    def wait(self) -> None:
-        _native.hip_check(self._hip.hipEventSynchronize(self._ev), "hipEventSynchronize")
+    def __init__(self, patience: float = 5.0):
+        self.host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
+        self._bytes = self.host.numpy()
+        self._ready = self._bytes[self._READY:self._READY + 4].view(np.uint32)
+        self.patience = patience
 
-    def __del__(self):
-        hip, ev = getattr(self, "_hip", None), getattr(self, "_ev", None)
-        if hip is not None and ev:
-            hip.hipEventDestroy(ev)
+    @property
+    def ptr(self) -> int:
+        return self.host.data_ptr()
+
+    def arm(self) -> None:
+        self._ready[0] = 0
+
+    def wait(self, stream: int) -> _native.StepScalars:
+        ready = self._ready
+        spins = 0
+        deadline = None
+        while ready[0] != 1:
+            spins += 1
+            if spins & 0x3FF == 0:
+                now = time.perf_counter()
+                if deadline is None:
+                    deadline = now + self.patience
+                elif now > deadline:
+                    _native.hip_check(_native.hip_runtime().hipStreamSynchronize(stream),
+                                      "hipStreamSynchronize")
+                    if ready[0] != 1:
+                        raise RuntimeError("the norm/clip kernel's host result did not arrive")
+                    break
+        return _native.StepScalars.from_buffer_copy(self._bytes.tobytes())
 
 
 class Workspace:
@@ -112,12 +130,11 @@ class Workspace:
         self.tile_sums: Optional[torch.Tensor] = None
         self.tile_flags: Optional[torch.Tensor] = None
         self._tile_streams: set = set()
-        # K2 also writes its result here (pinned host memory the device
-        # writes directly), so the read-back is a wait on an event recorded
-        # after K2 (HostWait): no copy, and K3, queued behind K2, keeps
+        # K2 also writes its result to pinned host memory, which the host
+        # polls (HostReadback): no copy, and K3, queued behind K2, keeps
         # running while the host does its bookkeeping
-        self.host = torch.empty(_native.SCALARS_BYTES, dtype=torch.uint8, pin_memory=True)
-        self._k2_done = HostWait(device)
+        self.readback = HostReadback()
+        self.host = self.readback.host
         self._stream: Optional[torch.cuda.Stream] = None   # stream of the last boundary
 
     def partial_ptrs(self, g: int):
@@ -161,16 +178,10 @@ class Workspace:
         self._stream = cur
         return cur
 
-    def start_readback(self) -> None:
-        """Mark the end of K2 (just launched on the current stream with
-        ``host`` as its host-side output)."""
-        self._k2_done.record(self._stream.cuda_stream)
-
     def finish_readback(self) -> _native.StepScalars:
-        """Wait for K2 (later kernels on the stream keep running) and read
-        the scalars it wrote to pinned host memory."""
-        self._k2_done.wait()
-        return _native.StepScalars.from_buffer_copy(self.host.numpy().tobytes())
+        """Wait for K2's scalars in pinned host memory (later kernels on the
+        stream keep running)."""
+        return self.readback.wait(self._stream.cuda_stream)
 
 
 class LaunchTimer:
@@ -339,6 +350,7 @@ def run_boundary(
         dtypes.append((gdtype, dtype, gbytes))
         flats.append(flat_out)
 
+    ws.readback.arm()
     tok = timer.start("k2")
     rc = lib.ms_norm_clip(
         ws.partials.data_ptr(), ws.flags.data_ptr(), ws.nblk, len(launches),
@@ -346,11 +358,10 @@ def run_boundary(
         1 if scaler.enabled else 0, float(scaler.scale), int(scaler.good_steps),
         int(scaler.skipped_steps), int(scaler.scale_window),
         float(scaler.min_scale), float(scaler.max_scale),
-        ws.scalars.data_ptr(), ws.host.data_ptr(), stream,
+        ws.scalars.data_ptr(), ws.readback.ptr, stream,
     )
     timer.stop(tok)
     _native.check(rc, "ms_norm_clip")
-    ws.start_readback()
 
     models = model_targets()
     for gl, (gdtype, dtype, gbytes), flat_out, mptrs in zip(launches, dtypes, flats, models):

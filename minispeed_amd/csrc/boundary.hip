@@ -141,6 +141,7 @@ constexpr int kScanWavesFlat = MS_SCAN_WAVES_FLAT;
 #endif
 constexpr int64_t kXcdChunk = MS_XCD_CHUNK;
 constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
+static_assert(kStatsBlocks % kNormThreads == 0, "K2 takes the same number of partials per thread");
 constexpr int kMaxSegs = 1 << 26;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -789,9 +790,27 @@ __global__ __launch_bounds__(kNormThreads) void k_norm_clip(
     const uint32_t* pf = bflag + static_cast<int64_t>(gi) * nblk;
     double acc = 0.0;
     uint32_t bad = 0;
-    for (int b = tid; b < nblk; b += kNormThreads) {
-      acc += ps[b];
-      bad |= pf[b];
+    if (nblk == kStatsBlocks) {
+      // all of a thread's partials in flight at once, then added in the
+      // same order as the loop below (slot tid, tid + kNormThreads, ...)
+      constexpr int kPer = kStatsBlocks / kNormThreads;
+      double x[kPer];
+      uint32_t f[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        x[i] = ps[tid + i * kNormThreads];
+        f[i] = pf[tid + i * kNormThreads];
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        acc += x[i];
+        bad |= f[i];
+      }
+    } else {
+      for (int b = tid; b < nblk; b += kNormThreads) {
+        acc += ps[b];
+        bad |= pf[b];
+      }
     }
     const double w = wave_sum(acc);
     const bool wb = __any(bad != 0);
@@ -815,7 +834,7 @@ __global__ __launch_bounds__(kNormThreads) void k_norm_clip(
 
   ms_step_scalars_t r;
   r.overflow = overflow ? 1u : 0u;
-  r.reserved = 0;
+  r.ready = 0;
   r.sumsq = total;
   r.norm = sqrtf(total);
   r.clip_applied = 0;
@@ -854,9 +873,13 @@ __global__ __launch_bounds__(kNormThreads) void k_norm_clip(
   r.next_skipped_steps = skipped;
   *out = r;
   if (out_host) {
-    // the host's copy, in pinned host memory: made visible system-wide
-    // before the kernel (and the event the host waits on) completes
+    // the host's copy, in pinned host memory: every field made visible
+    // system-wide, then `ready` set, so a host that sees ready == 1 reads
+    // the whole result (it may poll that word instead of waiting for the
+    // kernel's completion)
     *out_host = r;
+    __threadfence_system();
+    *static_cast<volatile uint32_t*>(&out_host->ready) = 1u;
     __threadfence_system();
   }
 }
@@ -1184,32 +1207,58 @@ __global__ __launch_bounds__(kStreamThreads) void k_accumulate(const AccumLaunch
 }
 
 // ------------------------------------------------------------------ K2a
-// One wave per partial slot j: the slot covers tiles [j*ntiles/nblk,
-// (j+1)*ntiles/nblk); lane l adds the tiles lo + l, lo + l + 64, ... in
+// Partial slot j covers tiles [j*ntiles/nblk, (j+1)*ntiles/nblk); lane l
+// of the wave that folds it adds the tiles lo + l, lo + l + 64, ... in
 // order, and the wave's fixed xor tree adds the lanes.  A fixed partition
-// and order, so the result is a pure function of the tile statistics; the
-// loads of a wave are consecutive slots of memory.
+// and order, so the result is a pure function of the tile statistics.  A
+// wave folds kFoldSlots consecutive slots; when no slot holds more than 64
+// tiles (every layout up to 2.1G flat indices per group) each lane has one
+// tile per slot, and all of the wave's loads are issued before the sums.
 constexpr int kFoldThreads = 256;
+constexpr int kFoldSlots = 4;
 
 __global__ __launch_bounds__(kFoldThreads) void k_fold_tiles(
     const double* __restrict__ ts, const uint32_t* __restrict__ tf, int64_t ntiles,
     double* __restrict__ bsum, uint32_t* __restrict__ bflag, int nblk) {
   const int lane = threadIdx.x & 63;
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * (kFoldThreads / 64) + (threadIdx.x >> 6);
-  if (j >= nblk) return;   // whole waves
-  const int64_t lo = j * ntiles / nblk;
-  const int64_t hi = (j + 1) * ntiles / nblk;
-  double total = 0.0;
-  uint32_t flag = 0;
-  for (int64_t k = lo + lane; k < hi; k += 64) {
-    total += ts[k];
-    flag |= tf[k];
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * (kFoldThreads / 64) + (threadIdx.x >> 6);
+  const int64_t j0 = w * kFoldSlots;
+  if (j0 >= nblk) return;   // whole waves
+  double total[kFoldSlots];
+  uint32_t flag[kFoldSlots];
+  if ((ntiles + nblk - 1) / nblk <= 64) {
+#pragma unroll
+    for (int s = 0; s < kFoldSlots; ++s) {
+      total[s] = 0.0;
+      flag[s] = 0;
+      const int64_t j = j0 + s;
+      const int64_t k = j * ntiles / nblk + lane;
+      if (j < nblk && k < (j + 1) * ntiles / nblk) {
+        total[s] += ts[k];
+        flag[s] = tf[k];
+      }
+    }
+  } else {
+    for (int s = 0; s < kFoldSlots; ++s) {
+      total[s] = 0.0;
+      flag[s] = 0;
+      const int64_t j = j0 + s;
+      if (j >= nblk) continue;
+      const int64_t hi = (j + 1) * ntiles / nblk;
+      for (int64_t k = j * ntiles / nblk + lane; k < hi; k += 64) {
+        total[s] += ts[k];
+        flag[s] |= tf[k];
+      }
+    }
   }
-  total = wave_sum(total);
-  const bool bad = __any(flag != 0);
-  if (lane == 0) {
-    bsum[j] = total;
-    bflag[j] = bad ? 1u : 0u;
+#pragma unroll
+  for (int s = 0; s < kFoldSlots; ++s) {
+    const double t = wave_sum(total[s]);
+    const bool bad = __any(flag[s] != 0);
+    if (lane == 0 && j0 + s < nblk) {
+      bsum[j0 + s] = t;
+      bflag[j0 + s] = bad ? 1u : 0u;
+    }
   }
 }
 
@@ -1315,7 +1364,7 @@ void launch_stats(const ms_segment_t* segs, int nseg, int64_t begin,
 // K2a over ntiles tile slots into nblk partial slots (all written)
 void launch_fold(const double* tsum, const uint32_t* tflag, int64_t ntiles, double* bsum,
                  uint32_t* bflag, int nblk, hipStream_t st) {
-  constexpr int kSlotsPerBlock = kFoldThreads / 64;
+  constexpr int kSlotsPerBlock = kFoldThreads / 64 * kFoldSlots;
   const dim3 grid((nblk + kSlotsPerBlock - 1) / kSlotsPerBlock);
   hipLaunchKernelGGL(k_fold_tiles, grid, dim3(kFoldThreads), 0, st, tsum, tflag, ntiles, bsum,
                      bflag, nblk);

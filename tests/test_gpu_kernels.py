@@ -334,7 +334,8 @@ def test_k4_cast_matches_torch_rounding(mdtype):
 
 def test_k2_host_copy_equals_device_result_after_an_event():
     """K2's optional host-side output (pinned memory written by the kernel)
-    holds the device result once an event recorded after K2 completes."""
+    holds the device result, with ``ready`` set, once an event recorded
+    after K2 completes."""
     lib = _native.load()
     nb = _native.stats_blocks()
     rng = np.random.default_rng(3)
@@ -351,8 +352,51 @@ def test_k2_host_copy_equals_device_result_after_an_event():
         ev.record()
         ev.synchronize()
         got = _native.StepScalars.from_buffer_copy(host.numpy().tobytes())
-        assert host.numpy().tobytes() == out.cpu().numpy().tobytes()
+        dev = _native.StepScalars.from_buffer_copy(out.cpu().numpy().tobytes())
+        assert got.ready == 1 and dev.ready == 0
+        dev.ready = 1
+        assert bytes(got) == bytes(dev)
         assert got.overflow == flag and got.next_good_steps == (0 if flag else k + 1)
+
+
+def test_k2_host_result_is_polled_while_later_kernels_run():
+    """The engine's read-back: ``ready`` cleared, K2 launched with the
+    pinned host output, K3 queued behind it; the host polls ``ready`` and
+    then reads the whole struct, equal to the device result, while the
+    stream may still be running K3 (HostReadback)."""
+    from minispeed_amd.boundary import HostReadback
+
+    lib = _native.load()
+    nb = _native.stats_blocks()
+    rng = np.random.default_rng(4)
+    ps = torch.from_numpy(rng.random(nb) * 1e-2).to(DEV)
+    pf = torch.zeros(nb, dtype=torch.int32, device=DEV)
+    out = torch.zeros(_native.SCALARS_BYTES, dtype=torch.uint8, device=DEV)
+    rb = HostReadback(patience=30.0)
+    n = 1 << 24
+    lay, p, m, v, grads = _adam_case([(n,)], F16, seed=1)
+    tab = Table(lay, 0, n, [store(g, off) for g, off in zip(_device(grads), lay.offsets)], [None])
+    dp, dm, dv = (torch.from_numpy(x.copy()).to(DEV) for x in (p, m, v))
+    lib_k3 = lib.ms_fused_adamw
+    for k, flag in enumerate((0, 1, 0, 0)):
+        pf[123] = flag
+        torch.cuda.synchronize()
+        rb.arm()
+        assert rb.host.numpy()[_native.StepScalars.ready.offset] == 0
+        rc = lib.ms_norm_clip(ps.data_ptr(), pf.data_ptr(), nb, 1, 1, 0.5, 1, 2.0 ** 16, k, 0, 1000,
+                              1.0, 2.0 ** 24, out.data_ptr(), rb.ptr, stream())
+        _native.check(rc, "ms_norm_clip")
+        hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, k + 1)
+        _native.check(lib_k3(dp.data_ptr(), dm.data_ptr(), dv.data_ptr(), None, tab.ptr, tab.nseg,
+                             _native.ms_dtype(F16), _native.ms_dtype(F16), 0, n, ctypes.byref(hp),
+                             out.data_ptr(), stream()), "ms_fused_adamw")
+        got = rb.wait(stream())
+        torch.cuda.synchronize()
+        dev = _native.StepScalars.from_buffer_copy(out.cpu().numpy().tobytes())
+        assert got.ready == 1
+        dev.ready = 1
+        assert bytes(got) == bytes(dev), k
+        assert got.overflow == flag
 
 
 def test_boundary_kernels_replay_in_a_hip_graph():
