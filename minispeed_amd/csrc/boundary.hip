@@ -140,6 +140,21 @@ constexpr int kScanWavesFlat = MS_SCAN_WAVES_FLAT;
 #define MS_XCD_CHUNK 1024
 #endif
 constexpr int64_t kXcdChunk = MS_XCD_CHUNK;
+// Gradient bytes K1 leaves in the Infinity Cache (MALL, 256 MB on MI355X)
+// for K3, which reads every gradient a second time.  K1's non-temporal loads
+// do not keep what they read there; K3's non-temporal accesses of the
+// masters, moments and model copy do not push out what is there.  So the
+// reading K1 takes the runs of its last kCacheKeepBytes of gradient with
+// ordinary loads (it reads them last, K3 reads them last) and K3 finds them
+// in the cache.  Over the fp16 GPT lists, in bench steps on one box: 124M
+// params 0.636 -> 0.618 ms, 350M 1.714 -> 1.694, 1.3B 6.228 -> 6.198 (K3
+// 5.792 -> 5.763, K1 +6 us); 96 / 160 / 224 / 320 MiB / every run: 124M
+// 0.634 / 0.627 / 0.619 / 0.620 / 0.619 ms, 1.3B 6.22 / 6.21 / 6.198 /
+// 6.200 / 6.237 (ordinary loads throughout slow K1 by 40 us there).
+#ifndef MS_CACHE_KEEP_MIB
+#define MS_CACHE_KEEP_MIB 224
+#endif
+constexpr int64_t kCacheKeepBytes = int64_t(MS_CACHE_KEEP_MIB) << 20;
 constexpr int kNormThreads = 1024;        // K2 block: 16 wave64
 static_assert(kStatsBlocks % kNormThreads == 0, "K2 takes the same number of partials per thread");
 constexpr int kMaxSegs = 1 << 26;
@@ -208,10 +223,16 @@ struct DBF16 {
 };
 
 // 16 bytes of raw gradient (8 fp16 / bf16 or 4 fp32 elements), 16-byte
-// aligned, as four 32-bit words, with the non-temporal hint (K1 reads each
-// gradient once).
+// aligned, as four 32-bit words: with the non-temporal hint, or (kKeep) as
+// an ordinary load, which leaves the lines in the Infinity Cache for K3
+// (kCacheKeepBytes below).
+template <bool kKeep = false>
 __device__ inline void load_unit(const void* p, uint32_t (&w)[4]) {
-  const u4 x = __builtin_nontemporal_load((const MS_GLOBAL u4*)p);
+  u4 x;
+  if constexpr (kKeep)
+    x = *((const MS_GLOBAL u4*)p);
+  else
+    x = __builtin_nontemporal_load((const MS_GLOBAL u4*)p);
 #pragma unroll
   for (int k = 0; k < 4; ++k) w[k] = x[k];
 }
@@ -443,7 +464,7 @@ __device__ inline float scale_grad(float g, float mul, float div) {
   else return g;
 }
 
-template <class G, bool kFlat, bool kStats, int kScale>
+template <class G, bool kFlat, bool kStats, int kScale, bool kKeep = false>
 struct GradScan {
   static constexpr int kScanDepth = kFlat ? MS_SCAN_DEPTH_FLAT : MS_SCAN_DEPTH_READ;
   static constexpr int kUnit = 16 / G::kBytes;   // elements per 16-byte unit
@@ -562,7 +583,7 @@ struct GradScan {
       uint32_t w[kScanDepth][4];
 #pragma unroll
       for (int d = 0; d < kScanDepth; ++d)
-        if (u + d * 64 < nu) load_unit(src + (u + d * 64) * 16, w[d]);
+        if (u + d * 64 < nu) load_unit<kKeep>(src + (u + d * 64) * 16, w[d]);
       add_ends();
 #pragma unroll
       for (int d = 0; d < kScanDepth; ++d) {
@@ -616,7 +637,8 @@ __device__ void scan_tile(Scan& sc, const ms_segment_t* segs, int nseg, int& s, 
 }
 
 // Reading only (kFlat false): each wave scans runs of `run` consecutive
-// tiles.  Writing the flat gradient (kFlat): one block of kScanWavesFlat
+// tiles; a run starting at tile keep_from or later is loaded with ordinary
+// loads (kCacheKeepBytes).  Writing the flat gradient (kFlat): one block of kScanWavesFlat
 // waves per tile.  A whole tile inside one segment with 16-byte aligned
 // storage, starting on a unit boundary of it and owned or not as a whole,
 // is split across the waves: wave w loads, widens and writes units
@@ -630,7 +652,7 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
     int64_t end, int64_t own_begin, int64_t own_end, float mul, float div,
     float* __restrict__ flat, double* __restrict__ tsum, uint32_t* __restrict__ tflag,
-    int64_t ntiles, int run) {
+    int64_t ntiles, int run, int64_t keep_from) {
   constexpr int kWaves = scan_waves<kFlat>();
   using Scan = GradScan<G, kFlat, kStats, kScale>;
   __shared__ f4 slabs[kFlat ? kWaves : 1][128];
@@ -646,17 +668,26 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
       const int64_t t1 = (t0 + run < ntiles) ? t0 + run : ntiles;
       // the cursor: the segment holding the next tile's first index
       int s = find_seg(segs, nseg, begin + t0 * kScanTile);
-      for (int64_t t = t0; t < t1; ++t) {
-        Scan sc;
-        sc.mul = mul;
-        sc.div = div;
-        sc.begin = begin;
-        sc.flat = (MS_GLOBAL float*)flat;
-        const int64_t r0 = begin + t * kScanTile;
-        const int64_t r1 = (r0 + kScanTile < end) ? r0 + kScanTile : end;
-        scan_tile<Scan, G, kStats>(sc, segs, nseg, s, t, r0, r1, own_begin, own_end, tsum,
-                                   tflag, lane);
-      }
+      // the run's load hint, a compile-time choice (a runtime one merges
+      // the two loads into one without the hint)
+      auto scan_run = [&](auto keep) {
+        using S = GradScan<G, kFlat, kStats, kScale, decltype(keep)::value>;
+        for (int64_t t = t0; t < t1; ++t) {
+          S sc;
+          sc.mul = mul;
+          sc.div = div;
+          sc.begin = begin;
+          sc.flat = (MS_GLOBAL float*)flat;
+          const int64_t r0 = begin + t * kScanTile;
+          const int64_t r1 = (r0 + kScanTile < end) ? r0 + kScanTile : end;
+          scan_tile<S, G, kStats>(sc, segs, nseg, s, t, r0, r1, own_begin, own_end, tsum,
+                                  tflag, lane);
+        }
+      };
+      if (t0 >= keep_from)
+        scan_run(BoolC<true>{});
+      else
+        scan_run(BoolC<false>{});
     }
   } else {
     constexpr int kUnit = Scan::kUnit;
@@ -1317,20 +1348,23 @@ void launch_stats_s(const ms_segment_t* segs, int nseg, int64_t begin, int64_t e
     if (flat) {
       hipLaunchKernelGGL((k_grad_stats<G, true, true, kScale>), dim3(scan_grid(ntiles, 1)),
                          dim3(64 * kScanWavesFlat), 0, st, segs, nseg, begin, end, ob, oe, mul,
-                         div, flat, tsum, tflag, ntiles, 1);
+                         div, flat, tsum, tflag, ntiles, 1, ntiles);
     } else {
       // runs of 2 and 4 tiles time alike over 60K-640K tiles, runs of 1 up
       // to 30% slower
       constexpr int kRun = MS_SCAN_RUN_READ;
+      // the tiles holding the last kCacheKeepBytes of gradient
+      const int64_t keep_tiles = kCacheKeepBytes / (int64_t(kScanTile) * G::kBytes);
+      const int64_t keep_from = ntiles > keep_tiles ? ntiles - keep_tiles : 0;
       hipLaunchKernelGGL((k_grad_stats<G, false, true, kScale>),
                          dim3(scan_grid(ntiles, kScanWavesRead * kRun)), dim3(64 * kScanWavesRead),
                          0, st, segs, nseg, begin, end, ob, oe, mul, div, flat, tsum, tflag,
-                         ntiles, kRun);
+                         ntiles, kRun, keep_from);
     }
   } else {
     hipLaunchKernelGGL((k_grad_stats<G, true, false, kScale>), dim3(scan_grid(ntiles, 1)),
                        dim3(64 * kScanWavesFlat), 0, st, segs, nseg, begin, end, ob, oe, mul, div,
-                       flat, tsum, tflag, ntiles, 1);
+                       flat, tsum, tflag, ntiles, 1, ntiles);
   }
 }
 
