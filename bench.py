@@ -52,13 +52,13 @@ METRIC = "boundary-step Gparams/s + HBM GB/s (% of peak) at 1.3B fp16, 1 GPU"
 PEAK_GBPS = 8000.0
 # HBM bytes per launch counted by two rocprofv3 --pmc runs of this file's
 # default workload and layout (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, both scales
-# calibrated on a 1 GiB device copy in the same runs; mean of 7 launches);
+# calibrated on a 1 GiB device copy in the same runs; mean of 10 launches);
 # commands and per-kernel counts in profiles/traffic_gpt-1.3b_fp16.md.  Keyed
 # by kernel / workload / grad dtype / mode / state window in GiB: a run in
 # any other configuration reports null.
 MEASURED_TRAFFIC = {
-    "k3/gpt-1.3b/fp16/fused/32.0": 36_844_935_793,
-    "k1/gpt-1.3b/fp16/fused/32.0": 2_639_428_710,
+    "k3/gpt-1.3b/fp16/fused/32.0": 36_844_767_232,
+    "k1/gpt-1.3b/fp16/fused/32.0": 2_639_888_384,
 }
 
 # algorithmic bytes per parameter: (K1, K3) for half / fp32 gradients
