@@ -312,9 +312,9 @@ __device__ inline bool quad_aligned(const void* p, int64_t elems, int bytes) {
 // the quad alignment of the flat tiles.  kind 0: aligned to the quad;
 // kind 1: 4-byte aligned (one access of 4-byte alignment, which global
 // memory takes for multi-dword loads and stores); kind 2: 2 mod 4 (2-byte
-// elements only), loaded as the three words around it, one element before
-// and one after the quad included, joined with alignbit, and stored as
-// 2 + 4 + 2 bytes.
+// elements only), loaded as the three words around the quad (ldq_any) and
+// stored a whole run of quads at a time as 8-byte aligned words passed
+// between neighbouring lanes (stq_run_kind2, below).
 typedef float f4w __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u2w __attribute__((ext_vector_type(2), aligned(4)));
 
@@ -343,6 +343,11 @@ __device__ inline void ldq_any(const void* p, int kind, float (&x)[4]) {
     const u2w w = __builtin_nontemporal_load((const MS_GLOBAL u2w*)p);
     widen_words<D>(w[0], w[1], x);
   } else {
+    // kind 2: the three words around the quad, one element before and one
+    // after it included (inside the tensor where the caller checked it),
+    // joined with alignbit.  (Whole words passed between neighbouring lanes,
+    // as the stores do, took K3 over the shifted 1.3B list from 5.88-5.91
+    // to 6.03-6.05 ms: each lane's shuffle waits for its load.)
     const MS_GLOBAL uint32_t* q = (const MS_GLOBAL uint32_t*)(static_cast<const char*>(p) - 2);
     const u2w lo = __builtin_nontemporal_load((const MS_GLOBAL u2w*)q);
     const uint32_t hi = __builtin_nontemporal_load(q + 2);
@@ -351,24 +356,55 @@ __device__ inline void ldq_any(const void* p, int kind, float (&x)[4]) {
   }
 }
 
+// kinds 0 and 1 (kind 2 of a 2-byte type: stq_run_kind2)
 template <class D>
 __device__ inline void stq_any(void* p, int kind, const float (&x)[4]) {
   if (kind == 0) {
     stq_raw<D>(p, x);
   } else if constexpr (D::kBytes == 4) {
     __builtin_nontemporal_store(f4w{x[0], x[1], x[2], x[3]}, (MS_GLOBAL f4w*)p);
-  } else {
+  } else {   // kind 1
     uint32_t w0, w1;
     narrow_words<D>(x, w0, w1);
-    if (kind == 1) {
-      __builtin_nontemporal_store(u2w{w0, w1}, (MS_GLOBAL u2w*)p);
-    } else {
-      MS_GLOBAL char* c = (MS_GLOBAL char*)p;
-      __builtin_nontemporal_store(static_cast<uint16_t>(w0), (MS_GLOBAL uint16_t*)c);
-      __builtin_nontemporal_store(__builtin_amdgcn_alignbit(w1, w0, 16),
-                                  (MS_GLOBAL uint32_t*)(c + 2));
-      __builtin_nontemporal_store(static_cast<uint16_t>(w1 >> 16), (MS_GLOBAL uint16_t*)(c + 6));
-    }
+    __builtin_nontemporal_store(u2w{w0, w1}, (MS_GLOBAL u2w*)p);
+  }
+}
+
+// The kind-2 stores of a run of kThreads consecutive quads of a 2-byte type,
+// quad j of the run held by thread j (K3's and K4's wave order), the run's
+// first element 2 mod 4 bytes off.  Stored quad by quad (2 + 4 + 2 bytes per
+// lane) every store instruction of a wave writes parts of lines: K3 over the
+// shifted 1.3B GPT list took 6.01 ms against 5.88-5.91 this way (aligned
+// list: 5.75).  Instead lane j joins the last 4 - s elements of its quad
+// with the first s of lane j + 1's (a wave shuffle) into the 8-byte aligned
+// word that starts at the run's element 4j + s (s = 1 or 3: the elements
+// before the first 8-byte boundary), so a wave's store covers a contiguous
+// run of whole lines.  The pieces no lane can complete go as single elements: the last 4
+// - s of each wave's last lane (the run's last, or the next wave's first s
+// elements finish the word) and the first s of each wave's first lane.
+// Every element of the run is written once; nothing outside it is touched.
+// All threads of the block must call this together.
+template <class D, int kThreads>
+__device__ inline void stq_run_kind2(void* run, int j, const float (&x)[4]) {
+  static_assert(D::kBytes == 2, "2-byte types only");
+  uint32_t w0, w1;
+  narrow_words<D>(x, w0, w1);
+  const int s = static_cast<int>(((8u - (reinterpret_cast<uintptr_t>(run) & 7u)) & 7u) >> 1);
+  const uint32_t n0 = __shfl_down(w0, 1u, 64), n1 = __shfl_down(w1, 1u, 64);
+  const uint64_t q = (static_cast<uint64_t>(w1) << 32) | w0;
+  const uint64_t qn = (static_cast<uint64_t>(n1) << 32) | n0;
+  MS_GLOBAL uint16_t* e = (MS_GLOBAL uint16_t*)run + 4 * j;   // the quad's first element
+  const int wl = j & 63;
+  if (wl != 63 && j != kThreads - 1) {
+    const uint64_t word = (q >> (16 * s)) | (qn << (16 * (4 - s)));
+    __builtin_nontemporal_store(word, (MS_GLOBAL uint64_t*)(e + s));
+  } else {
+    for (int k = s; k < 4; ++k)
+      __builtin_nontemporal_store(static_cast<uint16_t>(q >> (16 * k)), e + k);
+  }
+  if (wl == 0) {
+    for (int k = 0; k < s; ++k)
+      __builtin_nontemporal_store(static_cast<uint16_t>(q >> (16 * k)), e + k);
   }
 }
 
@@ -1010,7 +1046,17 @@ __global__ __launch_bounds__(kAdamThreads) void k_adamw(
         stq(master + tl + e, p[u]);
         stq(exp_avg + tl + e, m[u]);
         stq(exp_avg_sq + tl + e, v[u]);
-        if (seg.model) stq_any<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, mk, p[u]);
+        if (seg.model) {
+          char* q = static_cast<char*>(seg.model) + (so + e) * M::kBytes;
+          if constexpr (M::kBytes == 2) {
+            if (mk == 2)
+              stq_run_kind2<M, kAdamThreads>(q - 4 * lane * M::kBytes, lane, p[u]);
+            else
+              stq_any<M>(q, mk, p[u]);
+          } else {
+            stq_any<M>(q, mk, p[u]);
+          }
+        }
       }
     } else {
       int sl = s;
@@ -1082,7 +1128,15 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
         const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
-        stq_any<M>(static_cast<char*>(seg.model) + (so + e) * M::kBytes, mk, x[u]);
+        char* q = static_cast<char*>(seg.model) + (so + e) * M::kBytes;
+        if constexpr (M::kBytes == 2) {
+          if (mk == 2)
+            stq_run_kind2<M, kStreamThreads>(q - 4 * lane * M::kBytes, lane, x[u]);
+          else
+            stq_any<M>(q, mk, x[u]);
+        } else {
+          stq_any<M>(q, mk, x[u]);
+        }
       }
     } else {
       int sl = s;

@@ -58,6 +58,18 @@ def _views(sizes, dtype, offsets, fill=0.0):
     return pool, views
 
 
+def _assert_outside_untouched(pool, views, fill):
+    """Every element of the pool that no view covers still holds ``fill``:
+    the kernels wrote nothing outside the tensors."""
+    covered = torch.zeros(pool.numel(), dtype=torch.bool)
+    base = pool.data_ptr()
+    for v in views:
+        i = (v.data_ptr() - base) // pool.element_size()
+        covered[i:i + v.numel()] = True
+    rest = pool.cpu()[~covered]
+    assert torch.all(rest == fill), "a kernel wrote outside the tensors"
+
+
 @pytest.mark.parametrize("dtype", [F16, BF16, F32])
 @pytest.mark.parametrize("head", range(8))
 def test_k1_every_head_length(dtype, head):
@@ -127,7 +139,7 @@ def test_k3_quads_of_every_kind_match_the_aligned_layout(gdtype, mdtype, flat_gr
         lay = layout_for(layout_sizes)
         n = lay.numel_padded
         _, gviews = _views(sizes, gdtype, g_offsets)
-        _, mviews = _views(sizes, mdtype, m_offsets, fill=7.0)
+        mpool, mviews = _views(sizes, mdtype, m_offsets, fill=7.0)
         for v, h in zip(gviews, host_g):
             v.copy_(h.to(DEV))
         gst = [None] * len(layout_sizes)
@@ -154,6 +166,7 @@ def test_k3_quads_of_every_kind_match_the_aligned_layout(gdtype, mdtype, flat_gr
         for i, j in enumerate(index):
             off = lay.offsets[j]
             out.append([x[off:off + sizes[i]].cpu() for x in (dp, dm, dv)] + [mviews[i].cpu()])
+        _assert_outside_untouched(mpool, mviews, 7.0)
         return out
 
     # packed, views at every element offset of 16 bytes
@@ -176,18 +189,24 @@ def test_k3_quads_of_every_kind_match_the_aligned_layout(gdtype, mdtype, flat_gr
 
 
 @pytest.mark.parametrize("mdtype", [F16, BF16, F32])
-def test_k4_model_copies_of_every_kind(mdtype):
+@pytest.mark.parametrize("shift", [0, 1, 2, 3])
+def test_k4_model_copies_of_every_kind(mdtype, shift):
+    """Shifts 1 and 3 put every whole tile of a 2-byte model type at 2 mod 4
+    bytes (the whole-word stores of the kind-2 path), 0 and 2 at kinds 0
+    and 1."""
     sizes = [5, 4 * 1024 + 3, 1, 8 * 1024, 3 * 1024 + 2, 7]
     lay = layout_for(sizes)
     n = lay.numel_padded
     per16 = 16 // torch.empty(0, dtype=mdtype).element_size()
-    _, mviews = _views(sizes, mdtype, [(i * 3) % per16 for i in range(len(sizes))], fill=9.0)
+    pool, mviews = _views(sizes, mdtype, [(i * 3 + shift) % per16 for i in range(len(sizes))],
+                          fill=9.0)
     flat = torch.randn(n, generator=torch.Generator().manual_seed(2)) * 3.0
     tab = Table(lay, 0, n, [None] * len(sizes),
                 [store(v, off) for v, off in zip(mviews, lay.offsets)])
     k4(tab, mdtype, flat.to(DEV), 0, n)
     for v, off, k in zip(mviews, lay.offsets, sizes):
         np.testing.assert_array_equal(bits(v), bits(flat[off:off + k].to(mdtype)))
+    _assert_outside_untouched(pool, mviews, 9.0)
 
 
 @pytest.mark.parametrize("dtype", [F16, BF16])
