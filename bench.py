@@ -96,6 +96,9 @@ def parse(argv=None):
                          "hooks add each micro-batch's gradients into the fp32 sums)")
     ap.add_argument("--zero-stage", type=int, default=1, choices=[0, 1, 2, 3],
                     help="ZeRO stage at world size 1 (3: also times the parameter gather)")
+    ap.add_argument("--stage3-gather-reuse", action="store_true",
+                    help="hip_boundary.stage3_gather_reuse: the ZeRO-3 gather skips the cast "
+                         "while the model buffer holds the cast of the current masters")
     ap.add_argument("--state-spacing-gib", type=_spacing, default="auto",
                     help="hip_boundary.state_spacing_gib of the engine: auto (the engine's default), "
                          "0 (separate allocations) or a window in GiB")
@@ -117,7 +120,7 @@ def parse(argv=None):
 
 
 def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1, state_spacing_gib="auto",
-                  gas: int = 1) -> dict:
+                  gas: int = 1, gather_reuse: bool = False) -> dict:
     cfg = {
         "train_micro_batch_size_per_gpu": 1,
         "gradient_accumulation_steps": gas,
@@ -131,7 +134,8 @@ def engine_config(grad_dtype: str, mode: str, zero_stage: int = 1, state_spacing
         "zero_optimization": {"stage": zero_stage},
         "hip_boundary": {"materialize_flat_grad": mode == "materialize",
                          "contiguous_gradients": mode == "contiguous",
-                         "state_spacing_gib": state_spacing_gib},
+                         "state_spacing_gib": state_spacing_gib,
+                         "stage3_gather_reuse": gather_reuse},
         "steps_per_print": 1000000,
     }
     if grad_dtype == "fp16":
@@ -611,7 +615,8 @@ def main(argv=None) -> int:
         module = nn.ParameterList(params)
         engine = ms.initialize(model=module, model_parameters=list(module),
                                config=engine_config(args.grad_dtype, args.mode, args.zero_stage, spacing,
-                                                    args.micro_batches))
+                                                    args.micro_batches,
+                                                    gather_reuse=args.stage3_gather_reuse))
         while len(grad_sets) < 2:
             grad_sets.append([(torch.randn(*s, generator=gen, device=dev) * (1e-3 * mult)).to(gdt)
                               for s in shapes])
@@ -796,6 +801,7 @@ def main(argv=None) -> int:
             "grad_dtype": args.grad_dtype,
             "model_dtype": args.grad_dtype,
             "zero_stage": args.zero_stage,
+            "stage3_gather_reuse": bool(args.stage3_gather_reuse and args.zero_stage == 3),
             "world_size": 1,
             "mode": args.mode,
             "state_spacing_gib": args.state_spacing_gib,

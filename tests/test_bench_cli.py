@@ -49,6 +49,7 @@ def test_engine_config_parses_to_the_workload(dtype, mode):
     assert cfg.materialize_flat_grad == (mode == "materialize")
     assert cfg.contiguous_gradients == (mode == "contiguous")
     assert cfg.state_spacing_bytes == 0
+    assert DeepSpeedConfig(bench.engine_config(dtype, mode, 3, 0, gather_reuse=True)).stage3_gather_reuse
     if dtype == "fp16":              # dynamic loss scale from 2^16
         assert cfg.loss_scale == 0.0 and cfg.initial_scale_power == 16
     assert DeepSpeedConfig(bench.engine_config(dtype, mode)).state_spacing_bytes == -1
