@@ -547,3 +547,58 @@ def test_random_layouts_with_misaligned_views_and_empty_params(seed):
             if b > a:
                 np.testing.assert_array_equal(bits(view.cpu()[a - off:b - off]),
                                               bits(want4[a - lo:b - lo]))
+
+
+# The reading K1 takes the runs holding the last 224 MiB of gradient with
+# ordinary loads (K3 then finds those lines in the Infinity Cache) and the
+# other runs with non-temporal loads; the writing K1 never keeps anything.
+KEEP_BYTES = 224 << 20
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+def test_k1_cache_keeping_runs_match_the_writing_scan(dtype):
+    """A layout past the keeping threshold, so that both kinds of run are
+    scanned: the reading and the writing K1 give the same tile sums and
+    flags bit for bit, the sums match exact fp64 sums of squares of the
+    unscaled values K1 wrote, and an inf / nan planted in a non-temporal run
+    and in a kept run flags exactly its tile."""
+    esize = torch.empty(0, dtype=dtype).element_size()
+    keep_tiles = KEEP_BYTES // (_native.SCAN_TILE * esize)
+    n_want = (keep_tiles + 3000) * _native.SCAN_TILE
+    shapes = [(n_want // 3 - 5,), (n_want // 3 + 11,), (n_want - 2 * (n_want // 3) + 7,)]
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    grads = [(torch.randn(*s, generator=gen, device=DEV) * 1e-2).to(dtype) for s in shapes]
+    lay, tab = _grad_table(shapes, grads)
+    n = lay.numel_padded
+    scale = 65536.0 if dtype == F16 else 1.0
+    if scale != 1.0:
+        for g in grads:
+            g.mul_(scale)
+    _, _, ts_read, tf_read = k1(tab, dtype, 0, n, 0, n, scale=scale, tiles=True)
+    flat = torch.full((n,), float("nan"), dtype=torch.float32, device=DEV)
+    _, _, ts_write, tf_write = k1(tab, dtype, 0, n, 0, n, scale=scale, flat=flat, tiles=True)
+    nt = ts_read.size
+    assert nt > keep_tiles + 1000
+    np.testing.assert_array_equal(ts_read.view(np.int64), ts_write.view(np.int64))
+    np.testing.assert_array_equal(tf_read, tf_write)
+    assert not tf_read.any()
+    want = torch.cat([g.float().reshape(-1) for g in grads]).div_(scale)
+    got = flat[:want.numel()]
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+    x = flat.cpu().numpy().astype(np.float64)
+    x[want.numel():] = 0.0
+    pad = nt * _native.SCAN_TILE - n
+    exact = np.pad(x * x, (0, pad)).reshape(nt, _native.SCAN_TILE).sum(axis=1)
+    np.testing.assert_allclose(ts_read, exact, rtol=1e-12, atol=0)
+    # one special value in a non-temporal run (first third) and one in a kept run (the end)
+    special = {torch.float16: (0x7C00, 0x7E00), torch.bfloat16: (0x7F80, 0x7FC0),
+               torch.float32: (0x7F800000, 0x7FC00000)}[dtype]
+    i0, i1 = 12_345, n_want - 17
+    lo_tile, hi_tile = (lay.offsets[0] + i0) // _native.SCAN_TILE, None
+    set_bits(grads[0], i0, special[0])
+    last = grads[2]
+    set_bits(last, last.numel() - 17, special[1])
+    hi_tile = (lay.offsets[2] + last.numel() - 17) // _native.SCAN_TILE
+    assert lo_tile < nt - keep_tiles - 4 and hi_tile >= nt - keep_tiles
+    _, _, _, tf = k1(tab, dtype, 0, n, 0, n, scale=scale, tiles=True)
+    assert set(np.flatnonzero(tf)) == {lo_tile, hi_tile}
