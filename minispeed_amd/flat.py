@@ -356,9 +356,16 @@ def _take_at(addr: int, nbytes: int, device: torch.device,
     elsewhere are held in ``spare`` (released by the caller) so that the
     next request moves on to a larger one."""
     for _ in range(_CARVE_TRIES):
+        reserved = torch.cuda.memory_reserved(device)
         t = torch.empty(nbytes, dtype=torch.uint8, device=device)
         if t.data_ptr() == addr:
             return t
+        if torch.cuda.memory_reserved(device) > reserved:
+            # a new segment: no free block of the pool serves the request
+            # (e.g. max_split_size_mb keeps the arena's block from being
+            # split); asking again would only allocate more
+            del t
+            return None
         spare.append(t)
     return None
 
@@ -433,8 +440,10 @@ def place_state(sizes: Sequence[Sequence[int]], device: torch.device,
     windows' unused part -- goes back to the allocator as free blocks that
     any later tensor allocated on the same stream can use.  If the
     allocator does not serve the slots from the arena (another free block
-    of the pool fits better each time, or expandable segments), the arena
-    stays one tensor.  Columns larger than the window are allocated
+    of the pool fits better each time, or a request would need a new
+    segment, as when ``max_split_size_mb`` keeps the arena's block whole),
+    the arena stays one tensor; with expandable segments the state is
+    allocated separately.  Columns larger than the window are allocated
     separately, and so is everything when the device lacks the free memory
     (with a log line).  The placement changes no result.
     """
