@@ -306,23 +306,32 @@ def bench_llama_shard(args) -> dict:
     # them by default
     master, m, v = state_buffers([[S, S, S]], dev, AUTO_SPACING)[0]
     master.normal_(0.0, 0.02, generator=gen)
-    grad = torch.empty(S, dtype=torch.bfloat16, device=dev)
-    for a in range(0, S, 1 << 27):   # bounded fp32 temporaries
-        b = min(S, a + (1 << 27))
-        grad[a:b] = torch.randn(b - a, generator=gen, device=dev) * 1e-4
+    # two gradient sets, taken in turn, as the 1.3B bench does (the same
+    # buffer every step would let a step's scan find the previous scan's
+    # last lines still in the Infinity Cache)
+    grads = []
+    for _ in range(2):
+        grad = torch.empty(S, dtype=torch.bfloat16, device=dev)
+        for a in range(0, S, 1 << 27):   # bounded fp32 temporaries
+            b = min(S, a + (1 << 27))
+            grad[a:b] = torch.randn(b - a, generator=gen, device=dev) * 1e-4
+        grads.append(grad)
     holder = torch.empty(S, dtype=torch.bfloat16, device=dev)
-    gs, ms_ = [], []
-    for off, n in zip(lay.offsets, numels):
-        a, b = max(off, lo), min(off + n, hi)
-        if b > a:
-            gs.append((grad.data_ptr() + (a - lo) * 2, (a, b), 2))
-            ms_.append((holder.data_ptr() + (a - lo) * 2, (a, b), 2))
-        else:
-            gs.append(None)
-            ms_.append(None)
-    table = lay.segments(lo, hi, gs, ms_)
-    check_table(table, lo, hi)
-    tdev = torch.from_numpy(table).to(dev)
+    tables = []
+    for grad in grads:
+        gs, ms_ = [], []
+        for off, n in zip(lay.offsets, numels):
+            a, b = max(off, lo), min(off + n, hi)
+            if b > a:
+                gs.append((grad.data_ptr() + (a - lo) * 2, (a, b), 2))
+                ms_.append((holder.data_ptr() + (a - lo) * 2, (a, b), 2))
+            else:
+                gs.append(None)
+                ms_.append(None)
+        table = lay.segments(lo, hi, gs, ms_)
+        check_table(table, lo, hi)
+        tables.append(torch.from_numpy(table).to(dev))
+    nseg = int(tables[0].shape[0])
     nb = _native.stats_blocks()
     psum = torch.empty(nb, dtype=torch.float64, device=dev)
     pflag = torch.empty(nb, dtype=torch.int32, device=dev)
@@ -337,9 +346,10 @@ def bench_llama_shard(args) -> dict:
         """K1 -> K2 -> K3 with the engine's one host wait: for K2's scalars,
         written straight to pinned host memory, while K3 runs on."""
         t = timer if timed else None
+        tdev = tables[k % 2]
         hp = adamw_params(1e-3, (0.9, 0.999), 1e-8, 0.01, k + 1)
         tok = t.start("k1") if t else None
-        _native.check(lib.ms_grad_stats(tdev.data_ptr(), len(table), _native.DTYPE_BF16, lo, hi,
+        _native.check(lib.ms_grad_stats(tdev.data_ptr(), nseg, _native.DTYPE_BF16, lo, hi,
                                         lo, hi, 0, 1.0, None, tsum.data_ptr(), tflag.data_ptr(),
                                         ntiles, psum.data_ptr(), pflag.data_ptr(), nb, stream),
                       "ms_grad_stats")
@@ -351,7 +361,7 @@ def bench_llama_shard(args) -> dict:
                                        stream), "ms_norm_clip")
         tok = t.start("k3") if t else None
         _native.check(lib.ms_fused_adamw(master.data_ptr(), m.data_ptr(), v.data_ptr(), None,
-                                         tdev.data_ptr(), len(table), _native.DTYPE_BF16,
+                                         tdev.data_ptr(), nseg, _native.DTYPE_BF16,
                                          _native.DTYPE_BF16, lo, hi, ctypes.byref(hp),
                                          scal.data_ptr(), stream), "ms_fused_adamw")
         if t:
@@ -360,19 +370,26 @@ def bench_llama_shard(args) -> dict:
 
     for k in range(args.warmup):
         step(k, False)
+    # the timed steps with nothing recorded between the kernels, then the
+    # same steps again with HIP events around K1 and K3 for their times
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
-        last = [step(args.warmup + k, True)]
+        last = [step(args.warmup + k, False)]
     torch.cuda.synchronize()
     step_s = [(time.perf_counter() - t0) / args.steps]
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(args.warmup + args.steps + k, True)
+    torch.cuda.synchronize()
+    ms_events = (time.perf_counter() - t0) / args.steps * 1e3
     res = last[0]
     # norm = sqrt(S * 1e-8) ~ 3.2 > clip 1.0: the clip path is exercised
     if res.overflow or not res.clip_applied:
         raise RuntimeError(f"unexpected step scalars: overflow={res.overflow} clip={res.clip_applied}")
 
     # cast-on-gather of the full model: fp32 masters (all ranks' shards) -> bf16 params
-    del grad, holder
+    del grads, grad, holder
     full = torch.randn(N, generator=gen, device=dev) * 0.02
     params16 = torch.empty(N, dtype=torch.bfloat16, device=dev)
     gtable = lay.segments(0, N, [None] * len(numels),
@@ -403,11 +420,12 @@ def bench_llama_shard(args) -> dict:
         "unit": "Gparams/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_with_kernel_events": round(ms_events, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic: bf16 grads N(0,1e-4), fp32 masters N(0,0.02)",
+        "data": "synthetic: two sets of bf16 grads N(0,1e-4) taken in turn, fp32 masters N(0,0.02)",
         "config": {"workload": "one rank's 1/8 shard of Llama-3-8B (rank 3 of 8, fused mode)",
                    "shard_params": S, "model_params": N, "tensors": len(shapes),
-                   "shard_segments": len(table), "bytes_per_param": 30},
+                   "shard_segments": nseg, "bytes_per_param": 30},
         "hbm_gbps": round(30 * S / (ms_step * 1e-3) / 1e9, 1),
         "kernel_ms": {"k1": round(float(np.mean(timer.durations_ms("k1"))), 4), "k3": round(k3, 4),
                       "cast_on_gather": round(cast, 4)},
