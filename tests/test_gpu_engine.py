@@ -529,6 +529,52 @@ def test_state_arena_windows():
     assert plain_place.arena_bytes == 0 and plain_place.returned_bytes == 0
 
 
+_ARENA_NO_SPLIT = r"""
+import json, torch
+from minispeed_amd.flat import place_state
+dev = torch.device("cuda", 0)
+mib = 1 << 20
+torch.zeros(1, device=dev)
+before = torch.cuda.memory_reserved(dev)
+bufs, where = place_state([[100 * mib, 100 * mib, 100 * mib]], dev, 512 * mib)
+grown = torch.cuda.memory_reserved(dev) - before
+ok = all(int(b.count_nonzero()) == 0 and b.numel() == 100 * mib for b in bufs[0])
+base = bufs[0][0].data_ptr()
+offs = [b.data_ptr() - base for b in bufs[0]]
+print(json.dumps({"arena": where.arena_bytes, "held": where.held_bytes,
+                  "returned": where.returned_bytes, "grown": grown, "zero": ok, "offs": offs}))
+"""
+
+
+def test_state_arena_when_the_allocator_will_not_split_it():
+    """With ``max_split_size_mb`` below the arena's size torch's caching
+    allocator never splits the arena's block, so the state slots cannot be
+    carved out of it: place_state stops at the first request that would
+    take a new segment and keeps the whole arena as one tensor (the windows
+    still 512 MiB apart), without allocating more.  Runs in a child process:
+    the allocator setting is read when the process first allocates."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    env = dict(os.environ)
+    env["PYTORCH_HIP_ALLOC_CONF"] = "max_split_size_mb:1024"
+    env.pop("PYTORCH_CUDA_ALLOC_CONF", None)
+    env.pop("PYTORCH_ALLOC_CONF", None)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run([sys.executable, "-c", _ARENA_NO_SPLIT], cwd=root, env=env,
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr[-2000:]
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    mib = 1 << 20
+    assert res["arena"] == 3 * 512 * mib and res["held"] == res["arena"] and res["returned"] == 0
+    assert res["offs"] == [0, 512 * mib, 1024 * mib] and res["zero"]
+    # the arena, plus the one segment the first carving request (a 400 MiB
+    # slot) took before the carve gave up
+    assert res["grown"] <= 3 * 512 * mib + 400 * mib, res["grown"]
+
+
 def test_two_groups_share_one_arena():
     module = nn.Sequential(nn.Linear(64, 32), nn.Linear(32, 8)).to(DEV)
     decay = [p for n, p in module.named_parameters() if n.endswith("weight")]
