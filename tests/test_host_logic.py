@@ -317,3 +317,82 @@ def test_schedule_functions_equal_the_oracle_schedule_bit_for_bit():
             for e in range(-1, 260):
                 ref.last_epoch = e
                 assert fn(spec, e) == ref.get_lr(), (trial, kind, e)
+
+
+# ------------------------------------------------------ K2's host read-back
+def _readback(patience):
+    """A HostReadback over ordinary host memory (pinned memory needs a GPU;
+    the polling logic does not)."""
+    from minispeed_amd import _native
+    from minispeed_amd.boundary import HostReadback
+
+    rb = object.__new__(HostReadback)
+    rb.host = torch.zeros(_native.SCALARS_BYTES, dtype=torch.uint8)
+    rb._bytes = rb.host.numpy()
+    rb._ready = rb._bytes[HostReadback._READY:HostReadback._READY + 4].view(np.uint32)
+    rb.patience = patience
+    return rb
+
+
+def test_host_readback_returns_once_the_ready_word_turns():
+    """wait() spins until the kernel's ready word is 1 and then returns the
+    struct the kernel wrote before it; arm() clears the word."""
+    import threading
+    import time
+
+    from minispeed_amd import _native
+
+    rb = _readback(patience=30.0)
+    rb._ready[0] = 1
+    rb.arm()
+    assert rb._ready[0] == 0
+    want = _native.StepScalars(overflow=0, clip_applied=1, sumsq=4.0, norm=2.0, coef=0.5, ready=0,
+                               coef64=0.5, next_scale=1024.0, next_good_steps=3, next_skipped_steps=1)
+
+    def kernel():
+        time.sleep(0.05)
+        raw = np.frombuffer(bytes(want), dtype=np.uint8)
+        rb._bytes[:] = raw
+        rb._ready[0] = 1                          # the word last, as K2 sets it
+
+    t = threading.Thread(target=kernel)
+    t.start()
+    got = rb.wait(stream=0)
+    t.join()
+    assert (got.ready, got.clip_applied, got.norm, got.coef64, got.next_scale, got.next_good_steps) == \
+        (1, 1, 2.0, 0.5, 1024.0, 3)
+
+
+def test_host_readback_falls_back_to_a_stream_sync_and_raises_if_nothing_arrived(monkeypatch):
+    """Past its patience wait() synchronises the stream (which also reports a
+    device error) and raises when the word is still not set; if the word
+    arrives with the synchronisation, the struct is returned."""
+    from minispeed_amd import _native
+
+    calls = []
+
+    class FakeHip:
+        def __init__(self, on_sync=None):
+            self.on_sync = on_sync
+
+        def hipStreamSynchronize(self, stream):
+            calls.append(stream)
+            if self.on_sync:
+                self.on_sync()
+            return 0
+
+    rb = _readback(patience=0.02)
+    rb.arm()
+    monkeypatch.setattr(_native, "hip_runtime", lambda: FakeHip())
+    with pytest.raises(RuntimeError, match="did not arrive"):
+        rb.wait(stream=77)
+    assert calls == [77]
+
+    rb.arm()
+
+    def land():
+        rb._ready[0] = 1
+
+    monkeypatch.setattr(_native, "hip_runtime", lambda: FakeHip(on_sync=land))
+    assert rb.wait(stream=78).ready == 1
+    assert calls == [77, 78]
