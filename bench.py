@@ -57,8 +57,8 @@ PEAK_GBPS = 8000.0
 # by kernel / workload / grad dtype / mode / state window in GiB: a run in
 # any other configuration reports null.
 MEASURED_TRAFFIC = {
-    "k3/gpt-1.3b/fp16/fused/32.0": 36_844_767_232,
-    "k1/gpt-1.3b/fp16/fused/32.0": 2_639_888_384,
+    "k3/gpt-1.3b/fp16/fused/40.0": 36_844_151_808,
+    "k1/gpt-1.3b/fp16/fused/40.0": 2_639_890_432,
 }
 
 # algorithmic bytes per parameter: (K1, K3) for half / fp32 gradients
@@ -451,8 +451,8 @@ def bench_hbm_ceilings(args) -> dict:
     independent of the boundary kernels: one read stream, one write stream,
     a copy, in-place read-modify-write of one and of three arrays (AdamW's
     p, m, v) and K3's whole mix (three read-modify-write arrays plus one read
-    and one write array), 4 GiB per array, the arrays 32 GiB apart (the
-    placement of the state arena).  Each mix is run over a grid of launch
+    and one write array), 4 GiB per array, the arrays 32 GiB apart in one
+    allocation (an arena of the kind the engine places its state in).  Each mix is run over a grid of launch
     shapes (threads per block, 16-byte vectors per lane, lane or wave order,
     non-temporal hints) and the fastest is reported; then K3 itself over
     2^30 elements in the same placement.  Median of 6 launches after 2, HIP
@@ -536,7 +536,7 @@ def bench_hbm_ceilings(args) -> dict:
         log(f"[bench] {name}: {best['gbps']:.0f} GB/s ({best})")
 
     # K3's access pattern (AdamW arithmetic, fp16 g and copy) on layouts of
-    # the state: p, m, v in three 32 GiB windows (the engine's arena), the
+    # the state: p, m, v in three 32 GiB windows of one allocation, the
     # same with XCD-ordered blocks, and the three interleaved per tile of T
     # elements in one array
     probe.msp_adam_layout.restype = ctypes.c_int

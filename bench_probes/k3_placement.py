@@ -5,8 +5,8 @@ moments placed in a chosen way: the measurement behind the state arena.
                                         [--warmup W] [--reps R]
 
 * ``arena``: the engine's default placement (``flat.place_state`` with the
-  32 GiB window: three windows of one 96 GiB allocation, the gaps handed
-  back to torch's allocator);
+  automatic window, 40 GiB: three windows of one 120 GiB allocation, the
+  gaps handed back to torch's allocator);
 * ``separate``: three allocations (``place_state`` with window 0);
 * ``packed``: one allocation holding the three arrays back to back.
 
@@ -44,7 +44,7 @@ def main(argv=None) -> int:
 
     from minispeed_amd import _native
     from minispeed_amd.boundary import LaunchTimer, adamw_params
-    from minispeed_amd.flat import place_state
+    from minispeed_amd.flat import AUTO_SPACING, place_state
 
     n = args.elements
     if n <= 0 or n % 512:
@@ -57,7 +57,7 @@ def main(argv=None) -> int:
         state = [whole[k * n:(k + 1) * n] for k in range(3)]
         placement = {"bytes": 12 * n}
     else:
-        bufs, where = place_state([[n, n, n]], dev, (32 << 30) if args.placement == "arena" else 0)
+        bufs, where = place_state([[n, n, n]], dev, AUTO_SPACING if args.placement == "arena" else 0)
         state = bufs[0]
         placement = {"window": where.window, "arena_bytes": where.arena_bytes,
                      "held_bytes": where.held_bytes, "returned_bytes": where.returned_bytes}

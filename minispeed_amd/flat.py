@@ -267,7 +267,7 @@ _ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
 # the window from the state's size (``auto_window``), 0 means separate
 # allocations, a positive value is the window in bytes.
 AUTO_SPACING = -1
-_AUTO_WINDOW = 32 << 30
+_AUTO_WINDOW = 40 << 30
 _AUTO_MIN_COLUMN = 256 << 20   # the Infinity Cache: smaller states stay cache resident
 _AUTO_MAX_SHARE = 0.5      # of the free device memory
 _ARENA_SLACK_BYTES = 1 << 30
@@ -296,14 +296,18 @@ def _column_bytes(sizes: Sequence[Sequence[int]]) -> List[int]:
 
 
 def auto_window(sizes: Sequence[Sequence[int]], free_bytes: Optional[int] = None) -> int:
-    """The window ``state_buffers`` uses by default: 32 GiB when the largest
-    column holds between 256 MiB and 32 GiB and the arena (three windows)
-    takes at most half of ``free_bytes`` (when given), else 0, separate
-    allocations.  Smaller states largely stay in the 256 MB Infinity Cache
-    between steps, where placement does not show (3.3M params: the same
-    step time either way); at 124M params (0.5 GB arrays) the arena takes
-    K3 from 0.61-0.63 to 0.54 ms; states over a window lie far apart
-    anyway."""
+    """The window ``state_buffers`` uses by default: 40 GiB when the largest
+    column holds between 256 MiB and 40 GiB and the arena (three windows,
+    120 GiB) takes at most half of ``free_bytes`` (when given), else 0,
+    separate allocations.  Smaller states largely stay in the 256 MB
+    Infinity Cache between steps, where placement does not show (3.3M
+    params: the same step time either way); at 124M params (0.5 GB arrays)
+    the arena takes K3 from 0.61-0.63 to 0.53 ms; states over a window lie
+    far apart anyway.  Window sizes over 1.3B-param steps, each size in
+    every position of a sequence of processes on a box (the driver places
+    an allocation according to what earlier processes left): 32 GiB
+    6.12-6.15 ms for the first process, 6.15-6.175 later; 40 GiB 6.07-6.10
+    and 6.14-6.155; 48 GiB 6.06-6.07 and 6.12-6.22."""
     if not sizes:
         return 0
     cols = _column_bytes(sizes)
@@ -426,17 +430,16 @@ def place_state(sizes: Sequence[Sequence[int]], device: torch.device,
     at the same offsets in every window.  The fused AdamW kernel reads and
     writes the masters, exp_avg and exp_avg_sq at the same flat index in
     lockstep, and on MI355X that streams fastest when the three lie far
-    apart in *physical* HBM.  The driver backs an allocation with naturally
-    aligned power-of-two blocks, so windows of 32 GiB at the start of a 96
-    GiB allocation (a 64 GiB and a 32 GiB block) are 32 GiB apart in
-    physical memory too.  Measured on the 1.3B-param state (three 4.9 GiB
-    arrays), K3 in the arena 5.7-5.8 ms; three separate allocations 6.2-6.9
-    ms; one allocation holding the three back to back 6.0-6.3 ms, with
-    staggers of 4 KiB to 1.5 GiB between them 6.2-6.3 ms; windows of 6 to
-    28 GiB inside one 64 GiB block 6.0-6.3 ms on one box.
+    apart in *physical* HBM (the same requests wait longer at the memory
+    side when they collide on channels and banks).  Measured on the
+    1.3B-param state (three 4.9 GiB arrays): K3 in the arena 5.67-5.76 ms
+    with 40 GiB windows, 5.72-5.76 with 32 GiB ones; three separate
+    allocations 6.1-6.9 ms; one allocation holding the three back to back
+    6.0-6.3 ms, with staggers of 4 KiB to 1.5 GiB between them 6.2-6.3 ms;
+    windows of 6 to 28 GiB inside one 64 GiB block 6.0-6.3 ms on one box.
 
     The arena is carved through torch's caching allocator (:func:`_carve`):
-    the state keeps only its slots, and the rest of the 96 GiB -- the
+    the state keeps only its slots, and the rest of the arena -- the
     windows' unused part -- goes back to the allocator as free blocks that
     any later tensor allocated on the same stream can use.  If the
     allocator does not serve the slots from the arena (another free block
