@@ -57,8 +57,8 @@ PEAK_GBPS = 8000.0
 # by kernel / workload / grad dtype / mode / state window in GiB: a run in
 # any other configuration reports null.
 MEASURED_TRAFFIC = {
-    "k3/gpt-1.3b/fp16/fused/40.0": 36_844_151_808,
-    "k1/gpt-1.3b/fp16/fused/40.0": 2_639_890_432,
+    "k3/gpt-1.3b/fp16/fused/36.0": 36_840_508_262,
+    "k1/gpt-1.3b/fp16/fused/36.0": 2_639_900_128,
 }
 
 # algorithmic bytes per parameter: (K1, K3) for half / fp32 gradients

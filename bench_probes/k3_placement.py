@@ -5,7 +5,7 @@ moments placed in a chosen way: the measurement behind the state arena.
                                         [--warmup W] [--reps R]
 
 * ``arena``: the engine's default placement (``flat.place_state`` with the
-  automatic window, 40 GiB: three windows of one 120 GiB allocation, the
+  automatic window, 36 GiB: three windows of one 108 GiB allocation, the
   gaps handed back to torch's allocator);
 * ``separate``: three allocations (``place_state`` with window 0);
 * ``packed``: one allocation holding the three arrays back to back.

@@ -32,12 +32,12 @@ it is not bitwise minispeed and is off by default.
 ``state_spacing_gib`` places the fp32 masters, exp_avg and exp_avg_sq of all
 groups: with a number of GiB they lie in one allocation (the state arena) of
 three windows of that size, array j at the start of window j; 0 gives three
-separate allocations; "auto" (the default) uses 40 GiB windows for states of
-256 MiB to 40 GiB per array when the 120 GiB arena takes at most half of
+separate allocations; "auto" (the default) uses 36 GiB windows for states of
+256 MiB to 36 GiB per array when the 108 GiB arena takes at most half of
 the free device memory, and separate allocations otherwise.  On MI355X the
 fused AdamW kernel streams the three arrays 5-15% faster when they lie far
-apart in physical memory (1.3B params: 5.67-5.76 against 6.1-6.9 ms for
-separate allocations; 124M params: 0.53 against 0.61-0.63 ms).  The arena is
+apart in physical memory (1.3B params: 5.64-5.74 against 6.1-6.9 ms for
+separate allocations; 124M params: 0.52 against 0.61-0.63 ms).  The arena is
 carved through torch's caching allocator: the state holds only its own
 bytes, and the rest of the arena goes back to the allocator as free blocks
 that later tensors of the process are served from (``engine.state_placement``

@@ -267,7 +267,7 @@ _ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
 # the window from the state's size (``auto_window``), 0 means separate
 # allocations, a positive value is the window in bytes.
 AUTO_SPACING = -1
-_AUTO_WINDOW = 40 << 30
+_AUTO_WINDOW = 36 << 30
 _AUTO_MIN_COLUMN = 256 << 20   # the Infinity Cache: smaller states stay cache resident
 _AUTO_MAX_SHARE = 0.5      # of the free device memory
 _ARENA_SLACK_BYTES = 1 << 30
@@ -296,18 +296,21 @@ def _column_bytes(sizes: Sequence[Sequence[int]]) -> List[int]:
 
 
 def auto_window(sizes: Sequence[Sequence[int]], free_bytes: Optional[int] = None) -> int:
-    """The window ``state_buffers`` uses by default: 40 GiB when the largest
-    column holds between 256 MiB and 40 GiB and the arena (three windows,
-    120 GiB) takes at most half of ``free_bytes`` (when given), else 0,
+    """The window ``state_buffers`` uses by default: 36 GiB when the largest
+    column holds between 256 MiB and 36 GiB and the arena (three windows,
+    108 GiB) takes at most half of ``free_bytes`` (when given), else 0,
     separate allocations.  Smaller states largely stay in the 256 MB
     Infinity Cache between steps, where placement does not show (3.3M
     params: the same step time either way); at 124M params (0.5 GB arrays)
     the arena takes K3 from 0.61-0.63 to 0.53 ms; states over a window lie
     far apart anyway.  Window sizes over 1.3B-param steps, each size in
     every position of a sequence of processes on a box (the driver places
-    an allocation according to what earlier processes left): 32 GiB
-    6.12-6.15 ms for the first process, 6.15-6.175 later; 40 GiB 6.07-6.10
-    and 6.14-6.155; 48 GiB 6.06-6.07 and 6.12-6.22."""
+    an allocation according to what earlier processes left), mean step:
+    32 GiB 6.16 ms, 34 GiB 6.19, 35 GiB 6.08, 36 GiB 6.10 (18 processes,
+    6.07-6.16), 37 GiB 6.08, 38 GiB 6.17, 40 GiB 6.14, 42 GiB 6.11, 44 GiB
+    6.09 (a 132 GiB arena, over half of the free memory beside a 1.3B
+    model), 48 GiB 6.15 (6.06-6.26).  36 GiB sits inside the good 35-37
+    GiB band."""
     if not sizes:
         return 0
     cols = _column_bytes(sizes)
@@ -432,8 +435,8 @@ def place_state(sizes: Sequence[Sequence[int]], device: torch.device,
     lockstep, and on MI355X that streams fastest when the three lie far
     apart in *physical* HBM (the same requests wait longer at the memory
     side when they collide on channels and banks).  Measured on the
-    1.3B-param state (three 4.9 GiB arrays): K3 in the arena 5.67-5.76 ms
-    with 40 GiB windows, 5.72-5.76 with 32 GiB ones; three separate
+    1.3B-param state (three 4.9 GiB arrays): K3 in the arena 5.64-5.74 ms
+    with 36 GiB windows, 5.72-5.76 with 32 GiB ones; three separate
     allocations 6.1-6.9 ms; one allocation holding the three back to back
     6.0-6.3 ms, with staggers of 4 KiB to 1.5 GiB between them 6.2-6.3 ms;
     windows of 6 to 28 GiB inside one 64 GiB block 6.0-6.3 ms on one box.

@@ -65,14 +65,14 @@ def test_byte_accounting_per_mode():
 
 
 def test_measured_traffic_only_for_the_measured_configuration():
-    k3 = bench.traffic_for("k3", "gpt-1.3b", "fp16", "fused", 40)
-    assert k3 == bench.MEASURED_TRAFFIC["k3/gpt-1.3b/fp16/fused/40.0"]
+    k3 = bench.traffic_for("k3", "gpt-1.3b", "fp16", "fused", 36)
+    assert k3 == bench.MEASURED_TRAFFIC["k3/gpt-1.3b/fp16/fused/36.0"]
     # 28 B/param: the counted traffic is the algorithmic traffic to 0.1%
     assert abs(k3 / (28 * 1_315_723_264) - 1) < 1e-3
     for other in (("k3", "gpt-1.3b", "fp16", "fused", 0), ("k3", "gpt-1.3b", "fp16", "fused", 32),
-                  ("k3", "gpt-1.3b", "bf16", "fused", 40),
-                  ("k3", "gpt-1.3b", "fp16", "materialize", 40),
-                  ("k3", "gpt2-124m", "fp16", "fused", 40)):
+                  ("k3", "gpt-1.3b", "bf16", "fused", 36),
+                  ("k3", "gpt-1.3b", "fp16", "materialize", 36),
+                  ("k3", "gpt2-124m", "fp16", "fused", 36)):
         assert bench.traffic_for(*other) is None
 
 

@@ -167,24 +167,24 @@ def test_state_arena_layout():
     assert starts == [[0, 32 << 30, 64 << 30]] and total == 96 << 30
 
 
-def test_auto_window_is_40_gib_for_states_of_256_mib_to_40_gib_per_array():
+def test_auto_window_is_36_gib_for_states_of_256_mib_to_36_gib_per_array():
     from minispeed_amd.flat import auto_window
 
     gib = 1 << 30
     n13 = 1_315_723_264                                       # 1.3B GPT: 4.9 GiB arrays
-    assert auto_window([[n13, n13, n13]]) == 40 * gib
+    assert auto_window([[n13, n13, n13]]) == 36 * gib
     n8 = 8_030_261_248                                        # Llama-3-8B whole: 29.9 GiB
-    assert auto_window([[n8, n8, n8]]) == 40 * gib
+    assert auto_window([[n8, n8, n8]]) == 36 * gib
     assert auto_window([[3_323_392] * 3]) == 0                # tiny LM: 13 MB arrays
-    assert auto_window([[124_439_808] * 3]) == 40 * gib       # GPT-2 small: 0.46 GiB arrays
-    assert auto_window([[(256 << 20) // 4] * 3]) == 40 * gib  # exactly 256 MiB
+    assert auto_window([[124_439_808] * 3]) == 36 * gib       # GPT-2 small: 0.46 GiB arrays
+    assert auto_window([[(256 << 20) // 4] * 3]) == 36 * gib  # exactly 256 MiB
     assert auto_window([[(256 << 20) // 4 - (1 << 20)] * 3]) == 0    # 252 MiB
-    assert auto_window([[n8 + n13] * 3]) == 40 * gib          # 34.8 GiB: fits a window
-    assert auto_window([[(40 * gib) // 4] * 3]) == 40 * gib   # exactly 40 GiB
-    assert auto_window([[(40 * gib) // 4 + 1] * 3]) == 0      # 40 GiB + one element (a 2 MiB slot)
-    assert auto_window([[n8 + 3 * n13] * 3]) == 0             # 44.6 GiB: separate
-    assert auto_window([[n13, n13, n13], [n13, n13, n13]]) == 40 * gib     # 9.8 GiB columns
+    assert auto_window([[n8 + n13] * 3]) == 36 * gib          # 34.8 GiB: fits a window
+    assert auto_window([[(36 * gib) // 4] * 3]) == 36 * gib   # exactly 36 GiB
+    assert auto_window([[(36 * gib) // 4 + 1] * 3]) == 0      # 36 GiB + one element (a 2 MiB slot)
+    assert auto_window([[n8 + 2 * n13] * 3]) == 0             # 39.7 GiB: separate
+    assert auto_window([[n13, n13, n13], [n13, n13, n13]]) == 36 * gib     # 9.8 GiB columns
     assert auto_window([]) == 0
-    # the 120 GiB arena only when it takes at most half of the free memory
-    assert auto_window([[n13, n13, n13]], free_bytes=240 * gib) == 40 * gib
-    assert auto_window([[n13, n13, n13]], free_bytes=239 * gib) == 0
+    # the 108 GiB arena only when it takes at most half of the free memory
+    assert auto_window([[n13, n13, n13]], free_bytes=216 * gib) == 36 * gib
+    assert auto_window([[n13, n13, n13]], free_bytes=215 * gib) == 0
