@@ -583,8 +583,8 @@ struct GradScan {
     // tail element, then its units.  Reading only, the two elements are
     // loaded first and added after the first body loads are issued, so a
     // piece costs one memory round trip, not three; writing (the tiles the
-    // split path of k_grad_stats leaves to the walk: segment edges, missing
-    // gradients, tiles off the storage's unit grid) they are added first,
+    // split paths of k_grad_stats leave to the walk: segment edges, missing
+    // gradients, storage off 16 bytes) they are added first,
     // which keeps the registers of that kernel, compiled for 8 waves per
     // SIMD, within bounds.
     const int64_t hi = a + lane, ti = bu + lane;
@@ -639,6 +639,107 @@ constexpr int scan_waves() { return kFlat ? kScanWavesFlat : kScanWavesRead; }
 template <bool kFlat>
 constexpr int scan_min_waves() { return kFlat ? MS_SCAN_MIN_WAVES_FLAT : MS_SCAN_MIN_WAVES; }
 
+// Writing the flat gradient: a whole tile [r0, r0 + kScanTile) of one
+// segment whose first element sits m (> 0) elements into a 16-byte unit of
+// the (16-byte aligned) storage, so that the tile is a head of nh = kUnit -
+// m elements, kScanTile / kUnit - 1 whole units and a tail of m elements —
+// the pieces the walk of scan_tile takes.  All the block's waves load the
+// units (lane l of wave w: units (w * kPerLane + k) * 64 + l) and stage the
+// widened values in tile order at F[kUnit - nh + i], which puts every unit
+// on a 16-byte boundary of F; wave 0 loads the head, wave 1 the tail.
+// After the barrier every wave writes 512 consecutive floats of the tile,
+// one float per lane and store (64 consecutive floats, whole lines), and
+// wave 0 adds the squares in the walk's order: lane l its head element,
+// its tail element, then units l, l + 64, ..., so the slot gets the bits
+// one wave alone gives it.
+template <class Scan, class G, bool kStats, int kScale, int kWaves>
+__device__ void split_tile_shifted(Scan& sc, const ms_segment_t& sg, int64_t r0, int64_t begin,
+                                   int m, bool owned, float* __restrict__ flat, int64_t t,
+                                   double* __restrict__ tsum, uint32_t* __restrict__ tflag,
+                                   MS_LDS float* F, MS_LDS uint32_t* wflag, int wave, int lane,
+                                   float mul, float div) {
+  constexpr int kUnit = Scan::kUnit;
+  constexpr int kUnits = kScanTile / kUnit - 1;          // whole units of the tile
+  constexpr int kPerLane = (kUnits + 64 * kWaves) / (64 * kWaves);
+  static_assert(kPerLane * 64 * kWaves == kUnits + 1, "one unit slot per lane and round");
+  static_assert(kWaves >= 2, "wave 0 loads the head, wave 1 the tail");
+  const int nh = kUnit - m;
+  const int off = kUnit - nh;                            // F index of tile element 0
+  const int64_t e0 = r0 - sg.begin;                      // storage element of tile element 0
+  const char* usrc = static_cast<const char*>(sg.grad) + (e0 + nh) * G::kBytes;
+  uint32_t w[kPerLane][4];
+#pragma unroll
+  for (int k = 0; k < kPerLane; ++k) {
+    const int u = (wave * kPerLane + k) * 64 + lane;
+    if (u < kUnits) load_unit(usrc + static_cast<int64_t>(u) * 16, w[k]);
+  }
+  // head (wave 0, lanes < nh) and tail (wave 1, lanes < m) elements
+  bool ebad = false;
+  const bool head = wave == 0 && lane < nh, tail = wave == 1 && lane < m;
+  if (head || tail) {
+    const int64_t e = head ? e0 + lane : e0 + kScanTile - m + lane;
+    const typename G::raw r = load_raw1<G>(sg.grad, e);
+    ebad = G::nonfinite(r);
+    F[head ? off + lane : kScanTile + lane] = scale_grad<kScale>(G::widen(r), mul, div);
+  }
+#pragma unroll
+  for (int k = 0; k < kPerLane; ++k) {
+    const int u = (wave * kPerLane + k) * 64 + lane;
+    if (u < kUnits) {
+      float g[kUnit];
+      sc.template widen<false>(w[k], g);
+      MS_LDS f4* d = (MS_LDS f4*)(F + kUnit * (u + 1));
+#pragma unroll
+      for (int q = 0; q < kUnit / 4; ++q) d[q] = f4{g[4 * q], g[4 * q + 1], g[4 * q + 2], g[4 * q + 3]};
+    }
+  }
+  if constexpr (kStats) {
+    const bool wb = __any(ebad || (sc.packed & G::kTop) != 0);
+    if (lane == 0) wflag[wave] = wb ? 1u : 0u;
+  }
+  __syncthreads();
+  MS_GLOBAL float* o = (MS_GLOBAL float*)flat + (r0 - begin);
+  constexpr int kPerWave = kScanTile / kWaves;
+#pragma unroll
+  for (int i = 0; i < kPerWave / 64; ++i) {
+    const int p = wave * kPerWave + i * 64 + lane;
+    __builtin_nontemporal_store(F[off + p], o + p);
+  }
+  if constexpr (kStats) {
+    if (wave == 0) {
+      double acc = 0.0;
+      if (owned) {
+        auto add = [&](float v) {
+          const double x = static_cast<double>(v);
+          acc = __builtin_fma(x, x, acc);
+        };
+        if (lane < nh) add(F[off + lane]);
+        if (lane < m) add(F[kScanTile + lane]);
+#pragma unroll 1
+        for (int u = lane; u < kUnits; u += 64) {
+          const MS_LDS f4* d = (const MS_LDS f4*)(F + kUnit * (u + 1));
+#pragma unroll
+          for (int q = 0; q < kUnit / 4; ++q) {
+            const f4 x = d[q];
+            add(x[0]);
+            add(x[1]);
+            add(x[2]);
+            add(x[3]);
+          }
+        }
+      }
+      const double tot = wave_sum(acc);
+      if (lane == 0) {
+        uint32_t f = 0;
+#pragma unroll
+        for (int d = 0; d < kWaves; ++d) f |= wflag[d];
+        tsum[t] = tot;
+        tflag[t] = f;
+      }
+    }
+  }
+}
+
 // Tile t = [r0, r1) by one wave: walk its segments from the cursor s (left
 // on the segment that holds r1 when that one goes on), then the tile's
 // statistics into its slot.
@@ -681,8 +782,10 @@ __device__ void scan_tile(Scan& sc, const ms_segment_t* segs, int nseg, int& s, 
 // w*k*64 + lane .. (k units per lane), each store covering whole lines; the
 // widened values wait in LDS, and after a barrier wave 0 adds each lane's
 // units l, l + 64, ... in index order — the order one wave scanning the
-// tile alone uses, so the slots get the same bits.  Any other tile is
-// scanned by wave 0 alone, as when reading.
+// tile alone uses, so the slots get the same bits.  Such a tile starting
+// inside a unit of its storage is split the same way with its head and
+// tail elements (split_tile_shifted).  Any other tile is scanned by wave 0
+// alone, as when reading.
 template <class G, bool kFlat, bool kStats, int kScale>
 __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) void k_grad_stats(
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
@@ -691,7 +794,10 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
     int64_t ntiles, int run, int64_t keep_from) {
   constexpr int kWaves = scan_waves<kFlat>();
   using Scan = GradScan<G, kFlat, kStats, kScale>;
-  __shared__ f4 slabs[kFlat ? kWaves : 1][128];
+  // writing: a tile's widened values (aligned tiles: one slab of 128 f4
+  // per wave; tiles off the storage's unit grid: the tile in order from
+  // float kUnit - head, which takes up to 8 floats of the last row)
+  __shared__ f4 slabs[kFlat ? kWaves + 1 : 1][128];
   const int lane = threadIdx.x & 63;
   // uniform across the wave, and known to be so by the compiler: the tile
   // bounds, the segment search and the piece bookkeeping stay scalar
@@ -751,21 +857,29 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
       const ms_segment_t sg = segs[s];
       const bool owned = own_begin <= r0 && r1 <= own_end;
       // a whole tile inside one segment, storage and flat output 16-byte
-      // aligned, the tile starting on a unit of the storage, owned or not
-      // as a whole
+      // aligned, owned or not as a whole
       const bool split = r1 - r0 == kScanTile && sg.grad != nullptr && aligned16(sg.grad) &&
                          sg.begin <= r0 && r1 <= seg_end(sg) &&
-                         ((r0 - sg.begin) & (kUnit - 1)) == 0 &&
                          aligned16((const void*)(flat + (r0 - begin))) &&
                          (owned || r1 <= own_begin || own_end <= r0);
       const int64_t tn = t + gridDim.x;
       if (!split) {
-        // the other tiles (segment edges, missing gradients, segments off
-        // the flat space's unit grid): wave 0 walks them as when reading
+        // the other tiles (segment edges, missing gradients, storage off
+        // 16 bytes): wave 0 walks them as when reading
         if (wave == 0)
           scan_tile<Scan, G, kStats>(sc, segs, nseg, s, t, r0, r1, own_begin, own_end, tsum,
                                      tflag, lane);
         if (tn < ntiles) snext = find_seg(segs, nseg, begin + tn * kScanTile);
+        continue;
+      }
+      // the tile's first element sits m elements into a unit of the storage
+      const int m = static_cast<int>((r0 - sg.begin) & (kUnit - 1));
+      if (m != 0) {
+        split_tile_shifted<Scan, G, kStats, kScale, kWaves>(
+            sc, sg, r0, begin, m, owned, flat, t, tsum, tflag, (MS_LDS float*)&slabs[0][0],
+            (MS_LDS uint32_t*)wflag, wave, lane, mul, div);
+        if (tn < ntiles) snext = find_seg(segs, nseg, begin + tn * kScanTile);
+        __syncthreads();   // the staged tile and flags are rewritten by the next tile
         continue;
       }
       const char* src = static_cast<const char*>(sg.grad) + (r0 - sg.begin) * G::kBytes;

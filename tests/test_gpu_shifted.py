@@ -6,7 +6,8 @@ later gradient and model copy off the 16-byte units of K1's tiles and the
 quads of K3's; gradient and model views can also start at any element of
 their storage.  The kernels keep those tiles on vector paths (K1: the walk
 of a tile's head, tail and units, its ends loaded with the first units,
-rounds predicated; when writing the flat gradient, the one-wave walk; K3 /
+rounds predicated; when writing the flat gradient, the tile split over
+the block's four waves with its head and tail staged in LDS; K3 /
 K4 / K5: quads of any alignment).  Checked here:
 
 * K1 for every head length and dtype: the flat gradient bit for bit against
