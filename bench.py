@@ -218,11 +218,14 @@ def cpu_baseline(shapes, grad_dtype: str, sample_params: int) -> dict:
 
 # the other single-GPU configurations: (workload, ZeRO stage) of the
 # reported short runs next to the headline, with what they stand for
+# (name, ZeRO stage, description, timed steps): about 50-100 ms of timed
+# steps each, so that the start of the timed loop (the first step's host
+# work before its first kernel) adds little to a step of 0.6 ms
 EXTRA_WORKLOADS = (
-    ("gpt2-124m", 2, "GPT-2 small (124M params, 148 tensors), fp16 grads x 2^16, ZeRO-2"),
-    ("gpt-350m", 0, "350M GPT (24 layers, d 1024, 292 tensors), fp16 grads x 2^16, ZeRO-0"),
+    ("gpt2-124m", 2, "GPT-2 small (124M params, 148 tensors), fp16 grads x 2^16, ZeRO-2", 100),
+    ("gpt-350m", 0, "350M GPT (24 layers, d 1024, 292 tensors), fp16 grads x 2^16, ZeRO-0", 50),
 )
-EXTRA_STEPS, EXTRA_WARMUP = 20, 5
+EXTRA_STEPS, EXTRA_WARMUP = 20, 5      # the Llama-3-8B shard (4.6 ms steps)
 
 
 def extra_workloads(args, run_engine, gen, dev, gdt, mult) -> dict:
@@ -237,20 +240,20 @@ def extra_workloads(args, run_engine, gen, dev, gdt, mult) -> dict:
     from minispeed_amd.workloads import numel, shapes_of
 
     out = {}
-    for name, stage, desc in EXTRA_WORKLOADS:
+    for name, stage, desc, steps in EXTRA_WORKLOADS:
         shapes = shapes_of(name)
         n = numel(shapes)
         sets = []
         old = args.zero_stage
         args.zero_stage = stage
         try:
-            r = run_engine("auto", EXTRA_STEPS, True, shapes=shapes, grad_sets=sets, warmup=EXTRA_WARMUP)
+            r = run_engine("auto", steps, True, shapes=shapes, grad_sets=sets, warmup=EXTRA_WARMUP)
         finally:
             args.zero_stage = old
         del sets
         torch.cuda.empty_cache()
         gbps = 30 * n / (r["ms_step"] * 1e-3) / 1e9
-        out[name] = {"desc": desc, "params": n, "zero_stage": stage, "steps": EXTRA_STEPS,
+        out[name] = {"desc": desc, "params": n, "zero_stage": stage, "steps": steps,
                      "ms_per_step": round(r["ms_step"], 4),
                      "value": round(n / (r["ms_step"] * 1e-3) / 1e9, 3), "unit": "Gparams/s",
                      "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_GBPS, 4),
