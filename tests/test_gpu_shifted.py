@@ -20,7 +20,8 @@ K4 / K5: quads of any alignment).  Checked here:
   and model element must be too);
 * K4's model copies of every kind against torch's casts, K5's gradient at
   2 mod 4 bytes against the fp32 sum;
-* an engine on a shifted GPT-like list against the oracle, step by step,
+* an engine on a shifted GPT-like list against the oracle, step by step;
+  with the flat gradient materialised against the fused mode, bit for bit;
   and ZeRO-3 (parameters gathered as views at odd offsets of one buffer)
   against stage 0 bit for bit.
 """
@@ -286,6 +287,41 @@ def test_engine_on_a_shifted_list_against_the_oracle(dtype, stage):
     master = g.data.cpu()
     for (off, p), n in zip(g._offsets, g._numels):
         np.testing.assert_array_equal(bits(p.detach().reshape(-1)), bits(master[off:off + n].to(tdt)))
+
+
+@pytest.mark.parametrize("stage", [1, 2])
+def test_materialized_flat_gradient_on_a_shifted_list_equals_fused(stage):
+    """Tensors of whole tiles behind odd-sized ones (K1 writing the flat
+    gradient splits those tiles over the block's waves, head and tail
+    staged in LDS): three fp16 boundaries with the fp32 flat gradient
+    materialised give bitwise the masters, moments, norms and model of the
+    fused mode."""
+    sizes = [3, 5 * TILE + 7, 64, 3 * TILE, 5, 4 * TILE + 1, 9 * TILE, 2]
+    runs = []
+    for materialize in (False, True):
+        gen = torch.Generator().manual_seed(8)
+        params = [nn.Parameter((torch.randn(n, generator=gen) * 0.02).to(DEV)) for n in sizes]
+        module = nn.ParameterList(params)
+        cfg = {"train_micro_batch_size_per_gpu": 1, "gradient_accumulation_steps": 1,
+               "gradient_clipping": 0.5, "dtype": "fp16", "zero_optimization": {"stage": stage},
+               "optimizer": {"type": "AdamW", "params": {"lr": 1e-3, "weight_decay": 0.01}},
+               "fp16": {"enabled": True, "loss_scale": 0, "initial_scale_power": 10},
+               "hip_boundary": {"materialize_flat_grad": materialize}, "steps_per_print": 1000}
+        engine = ms.initialize(model=module, model_parameters=list(module), config=cfg)
+        norms = []
+        for _ in range(3):
+            for p, n in zip(params, sizes):
+                p.grad = (torch.randn(n, generator=gen) * 1e-2 * 2.0 ** 10).to(DEV).half()
+            engine.micro_steps += 1
+            assert engine.step() is True
+            norms.append(engine.grad_norm)
+        st = engine.optimizer.state[0]
+        runs.append(([engine.flat_groups[0].data.clone(), st["exp_avg"].clone(),
+                      st["exp_avg_sq"].clone()] + [p.detach().clone() for p in params], norms))
+    (a, na), (b, nb) = runs
+    assert na == nb and any(n > 0.5 for n in na)      # the clip ran
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.int8), y.view(torch.int8))
 
 
 def test_zero3_on_a_shifted_list_equals_stage0():
