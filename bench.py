@@ -1,6 +1,6 @@
 """Boundary-step throughput of minispeed_amd on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5]
                     [--workload gpt-1.3b | gpt-1.3b-shift3 | llama3-8b-shard | ...]
                     [--grad-dtype fp16] [--mode fused|materialize|contiguous] [--micro-batches 1]
                     [--zero-stage 1]
@@ -14,7 +14,8 @@ the host bookkeeping.  Before each step one of two pre-generated gradient
 sets, resident in HBM, is re-attached to ``param.grad`` (what the last
 ``backward`` of a window leaves).  The K timed steps run back to back,
 bracketed as a whole by ``torch.cuda.synchronize()``; ``ms_per_step`` is
-the bracket over K.  The same steps are then run one at a time, each
+the bracket over K (so the first step's host work before its first kernel,
+0.1-0.3 ms, adds that over K to each step: K defaults to 50).  The same steps are then run one at a time, each
 bracketed on its own (``ms_per_step_synced``: the latency of one boundary,
 host work before the first kernel included).  With ``--mode contiguous``
 the accumulation kernels of the gradient hooks (backward work on the same
@@ -86,7 +87,7 @@ def _spacing(text: str):
 def parse(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gpt-1.3b")
     ap.add_argument("--grad-dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
