@@ -376,37 +376,61 @@ __device__ inline void stq_any(void* p, int kind, const float (&x)[4]) {
 // lane) every store instruction of a wave writes parts of lines: K3 over the
 // shifted 1.3B GPT list took 6.01 ms against 5.88-5.91 this way (aligned
 // list: 5.75).  Instead lane j joins the last 4 - s elements of its quad
-// with the first s of lane j + 1's (a wave shuffle) into the 8-byte aligned
-// word that starts at the run's element 4j + s (s = 1 or 3: the elements
-// before the first 8-byte boundary), so a wave's store covers a contiguous
-// run of whole lines.  The pieces no lane can complete go as single elements: the last 4
-// - s of each wave's last lane (the run's last, or the next wave's first s
-// elements finish the word) and the first s of each wave's first lane.
-// Every element of the run is written once; nothing outside it is touched.
-// All threads of the block must call this together.
+// with the first s of lane j + 1's into the 8-byte aligned word that starts
+// at the run's element 4j + s (s = 1 or 3: the elements before the first
+// 8-byte boundary), so a wave's store covers a contiguous run of whole
+// lines.  Within a wave the neighbour's quad comes by a shuffle; across a
+// wave boundary through `xq` (LDS, two words per wave of the block): the
+// first lane of each later wave hands its quad to the previous wave's last
+// lane, so the line at a wave boundary is written whole by one wave, not in
+// two pieces (the memory completes a partial line by reading it first: K3
+// on the shifted list 5.85-5.88 ms with the pieces, 5.70-5.72 ms without).
+// Only the run's ends go as single elements: the last 4 - s of the run's
+// last lane and the first s of its first lane.  Every element of the run is
+// written once; nothing outside it is touched.  All threads of the block
+// call this together (it holds a barrier); consecutive calls alternate
+// between two `xq` buffers, so a wave that runs ahead does not overwrite a
+// hand-over before it is read.
 template <class D, int kThreads>
-__device__ inline void stq_run_kind2(void* run, int j, const float (&x)[4]) {
+__device__ inline void stq_run_kind2(void* run, int j, const float (&x)[4],
+                                     MS_LDS uint32_t* __restrict__ xq) {
   static_assert(D::kBytes == 2, "2-byte types only");
   uint32_t w0, w1;
   narrow_words<D>(x, w0, w1);
   const int s = static_cast<int>(((8u - (reinterpret_cast<uintptr_t>(run) & 7u)) & 7u) >> 1);
-  const uint32_t n0 = __shfl_down(w0, 1u, 64), n1 = __shfl_down(w1, 1u, 64);
+  uint32_t n0 = __shfl_down(w0, 1u, 64), n1 = __shfl_down(w1, 1u, 64);
+  const int wl = j & 63;
+  if (wl == 0 && j != 0) {
+    xq[2 * ((j >> 6) - 1)] = w0;
+    xq[2 * ((j >> 6) - 1) + 1] = w1;
+  }
+  __syncthreads();
+  if (wl == 63 && j != kThreads - 1) {
+    n0 = xq[2 * (j >> 6)];
+    n1 = xq[2 * (j >> 6) + 1];
+  }
   const uint64_t q = (static_cast<uint64_t>(w1) << 32) | w0;
   const uint64_t qn = (static_cast<uint64_t>(n1) << 32) | n0;
   MS_GLOBAL uint16_t* e = (MS_GLOBAL uint16_t*)run + 4 * j;   // the quad's first element
-  const int wl = j & 63;
-  if (wl != 63 && j != kThreads - 1) {
+  if (j != kThreads - 1) {
     const uint64_t word = (q >> (16 * s)) | (qn << (16 * (4 - s)));
     __builtin_nontemporal_store(word, (MS_GLOBAL uint64_t*)(e + s));
   } else {
     for (int k = s; k < 4; ++k)
       __builtin_nontemporal_store(static_cast<uint16_t>(q >> (16 * k)), e + k);
   }
-  if (wl == 0) {
+  if (j == 0) {
     for (int k = 0; k < s; ++k)
       __builtin_nontemporal_store(static_cast<uint16_t>(q >> (16 * k)), e + k);
   }
 }
+
+// LDS of stq_run_kind2's hand-overs for a block of kThreads: two buffers of
+// two words per wave
+template <int kThreads>
+struct Kind2Lds {
+  uint32_t w[2][2 * (kThreads / 64)];
+};
 
 template <class D>
 __device__ inline typename D::raw load_raw1(const void* base, int64_t k) {
@@ -1115,6 +1139,8 @@ __global__ __launch_bounds__(kAdamThreads) void k_adamw(
   const bool arrays_vec = aligned16(master) && aligned16(exp_avg) &&
                           aligned16(exp_avg_sq) &&
                           (!kFlatGrad || aligned16(flat_grad));
+  __shared__ Kind2Lds<kAdamThreads> k2lds;
+  int k2buf = 0;   // the buffer of the next kind-2 run
 
   for (int64_t t = xcd_tile(blockIdx.x, gridDim.x, kXcdChunk); t < ntiles; t += gridDim.x) {
     const int64_t t0 = begin + t * kAdamTile;
@@ -1163,10 +1189,13 @@ __global__ __launch_bounds__(kAdamThreads) void k_adamw(
         if (seg.model) {
           char* q = static_cast<char*>(seg.model) + (so + e) * M::kBytes;
           if constexpr (M::kBytes == 2) {
-            if (mk == 2)
-              stq_run_kind2<M, kAdamThreads>(q - 4 * lane * M::kBytes, lane, p[u]);
-            else
+            if (mk == 2) {
+              stq_run_kind2<M, kAdamThreads>(q - 4 * lane * M::kBytes, lane, p[u],
+                                             (MS_LDS uint32_t*)k2lds.w[k2buf]);
+              k2buf ^= 1;
+            } else {
               stq_any<M>(q, mk, p[u]);
+            }
           } else {
             stq_any<M>(q, mk, p[u]);
           }
@@ -1210,6 +1239,8 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
   const int64_t n = end - begin;
   const int64_t ntiles = (n + kStreamTile - 1) / kStreamTile;
   const bool flat_vec = aligned16(flat);
+  __shared__ Kind2Lds<kStreamThreads> k2lds;
+  int k2buf = 0;   // the buffer of the next kind-2 run
   for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
     const int64_t t0 = begin + t * kStreamTile;
     const int64_t t1 = (t0 + kStreamTile < end) ? t0 + kStreamTile : end;
@@ -1244,10 +1275,13 @@ __global__ __launch_bounds__(kStreamThreads) void k_cast(
         const int64_t e = 4 * (static_cast<int64_t>(u) * kStreamThreads + lane);
         char* q = static_cast<char*>(seg.model) + (so + e) * M::kBytes;
         if constexpr (M::kBytes == 2) {
-          if (mk == 2)
-            stq_run_kind2<M, kStreamThreads>(q - 4 * lane * M::kBytes, lane, x[u]);
-          else
+          if (mk == 2) {
+            stq_run_kind2<M, kStreamThreads>(q - 4 * lane * M::kBytes, lane, x[u],
+                                             (MS_LDS uint32_t*)k2lds.w[k2buf]);
+            k2buf ^= 1;
+          } else {
             stq_any<M>(q, mk, x[u]);
+          }
         } else {
           stq_any<M>(q, mk, x[u]);
         }
