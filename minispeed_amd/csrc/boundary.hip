@@ -524,8 +524,19 @@ __device__ inline float scale_grad(float g, float mul, float div) {
   else return g;
 }
 
-template <class G, bool kFlat, bool kStats, int kScale, bool kKeep = false>
+// kSumFlags: the inf/nan flag of the counted elements' 16-byte units comes
+// from their fp64 sum of squares instead of a test of every word.  Exact
+// when the scaling cannot turn a finite gradient into inf (none, a multiply
+// by at most 1, a division by at least 1): an inf/nan element then squares
+// to inf/nan and the sum is inf/nan, while finite elements (fp32 at most
+// 3.4e38) square and add up to at most ~1e81 in fp64; the sum of squares is
+// non-negative, so inf never meets -inf.  Elements outside the owned range
+// (not counted) are still tested one by one.
+template <class G, bool kFlat, bool kStats, int kScale, bool kKeep = false,
+          bool kSumFlags = false>
 struct GradScan {
+  static_assert(!kSumFlags || kStats, "the flags come from the statistics");
+  static constexpr bool kFlagsFromSum = kSumFlags;
   static constexpr int kScanDepth = kFlat ? MS_SCAN_DEPTH_FLAT : MS_SCAN_DEPTH_READ;
   static constexpr int kUnit = 16 / G::kBytes;   // elements per 16-byte unit
   float mul, div;
@@ -560,8 +571,10 @@ struct GradScan {
   // four 32-bit words, widened (and counted) into g.
   template <bool kCount>
   __device__ void widen(const uint32_t (&w)[4], float (&g)[kUnit]) {
+    if constexpr (!(kSumFlags && kCount && kStats)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) packed |= (w[j] & G::kExp) + G::kExpOne;
+      for (int j = 0; j < 4; ++j) packed |= (w[j] & G::kExp) + G::kExpOne;
+    }
 #pragma unroll
     for (int k = 0; k < kUnit; ++k) {
       g[k] = scale_grad<kScale>(G::widen(unit_elem<G>(w, k)), mul, div);
@@ -787,7 +800,8 @@ __device__ void scan_tile(Scan& sc, const ms_segment_t* segs, int nseg, int& s, 
     if (se > r1) break;   // it also holds the next tile's first index
   }
   if (kStats) {
-    const bool bad = sc.bad || (sc.packed & G::kTop) != 0;
+    bool bad = sc.bad || (sc.packed & G::kTop) != 0;
+    if constexpr (Scan::kFlagsFromSum) bad = bad || !__builtin_isfinite(sc.acc);
     const double w = wave_sum(sc.acc);
     const bool wb = __any(bad);
     if (lane == 0) {
@@ -810,12 +824,13 @@ __device__ void scan_tile(Scan& sc, const ms_segment_t* segs, int nseg, int& s, 
 // inside a unit of its storage is split the same way with its head and
 // tail elements (split_tile_shifted).  Any other tile is scanned by wave 0
 // alone, as when reading.
-template <class G, bool kFlat, bool kStats, int kScale>
+template <class G, bool kFlat, bool kStats, int kScale, bool kSumFlags = false>
 __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) void k_grad_stats(
     const ms_segment_t* __restrict__ segs, int nseg, int64_t begin,
     int64_t end, int64_t own_begin, int64_t own_end, float mul, float div,
     float* __restrict__ flat, double* __restrict__ tsum, uint32_t* __restrict__ tflag,
     int64_t ntiles, int run, int64_t keep_from) {
+  static_assert(!(kFlat && kSumFlags), "writing, the flags come from the per-word tests");
   constexpr int kWaves = scan_waves<kFlat>();
   using Scan = GradScan<G, kFlat, kStats, kScale>;
   // writing: a tile's widened values (aligned tiles: one slab of 128 f4
@@ -837,7 +852,7 @@ __global__ __launch_bounds__(64 * scan_waves<kFlat>(), scan_min_waves<kFlat>()) 
       // the run's load hint, a compile-time choice (a runtime one merges
       // the two loads into one without the hint)
       auto scan_run = [&](auto keep) {
-        using S = GradScan<G, kFlat, kStats, kScale, decltype(keep)::value>;
+        using S = GradScan<G, kFlat, kStats, kScale, decltype(keep)::value, kSumFlags>;
         for (int64_t t = t0; t < t1; ++t) {
           S sc;
           sc.mul = mul;
@@ -1558,10 +1573,20 @@ void launch_stats_s(const ms_segment_t* segs, int nseg, int64_t begin, int64_t e
       // the tiles holding the last kCacheKeepBytes of gradient
       const int64_t keep_tiles = kCacheKeepBytes / (int64_t(kScanTile) * G::kBytes);
       const int64_t keep_from = ntiles > keep_tiles ? ntiles - keep_tiles : 0;
-      hipLaunchKernelGGL((k_grad_stats<G, false, true, kScale>),
-                         dim3(scan_grid(ntiles, kScanWavesRead * kRun)), dim3(64 * kScanWavesRead),
-                         0, st, segs, nseg, begin, end, ob, oe, mul, div, flat, tsum, tflag,
-                         ntiles, kRun, keep_from);
+      // the counted elements' flags from their sums wherever the scaling
+      // cannot overflow a finite gradient (GradScan's kSumFlags)
+      const bool sum_flags = kScale == kScaleNone || (kScale == kScaleMul && mul <= 1.0f) ||
+                             (kScale == kScaleDiv && div >= 1.0f);
+      auto go = [&](auto sf) {
+        hipLaunchKernelGGL((k_grad_stats<G, false, true, kScale, decltype(sf)::value>),
+                           dim3(scan_grid(ntiles, kScanWavesRead * kRun)),
+                           dim3(64 * kScanWavesRead), 0, st, segs, nseg, begin, end, ob, oe, mul,
+                           div, flat, tsum, tflag, ntiles, kRun, keep_from);
+      };
+      if (sum_flags)
+        go(BoolC<true>{});
+      else
+        go(BoolC<false>{});
     }
   } else {
     hipLaunchKernelGGL((k_grad_stats<G, true, false, kScale>), dim3(scan_grid(ntiles, 1)),
