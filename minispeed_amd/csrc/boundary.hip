@@ -527,7 +527,7 @@ __device__ inline float scale_grad(float g, float mul, float div) {
 // kSumFlags: the inf/nan flag of the counted elements' 16-byte units comes
 // from their fp64 sum of squares instead of a test of every word.  Exact
 // when the scaling cannot turn a finite gradient into inf (none, a multiply
-// by at most 1, a division by at least 1): an inf/nan element then squares
+// by a factor in [-1, 1], a division by at least 1): an inf/nan element then squares
 // to inf/nan and the sum is inf/nan, while finite elements (fp32 at most
 // 3.4e38) square and add up to at most ~1e81 in fp64; the sum of squares is
 // non-negative, so inf never meets -inf.  Elements outside the owned range
@@ -1575,7 +1575,8 @@ void launch_stats_s(const ms_segment_t* segs, int nseg, int64_t begin, int64_t e
       const int64_t keep_from = ntiles > keep_tiles ? ntiles - keep_tiles : 0;
       // the counted elements' flags from their sums wherever the scaling
       // cannot overflow a finite gradient (GradScan's kSumFlags)
-      const bool sum_flags = kScale == kScaleNone || (kScale == kScaleMul && mul <= 1.0f) ||
+      const bool sum_flags = kScale == kScaleNone ||
+                             (kScale == kScaleMul && mul >= -1.0f && mul <= 1.0f) ||
                              (kScale == kScaleDiv && div >= 1.0f);
       auto go = [&](auto sf) {
         hipLaunchKernelGGL((k_grad_stats<G, false, true, kScale, decltype(sf)::value>),

@@ -332,6 +332,41 @@ def test_k4_cast_matches_torch_rounding(mdtype):
     np.testing.assert_array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+@pytest.mark.parametrize("factor", [1e36, -1e36, 3.0, -1.0, -0.5, 0.0])
+def test_k1_flags_follow_the_raw_gradients_under_any_factor(dtype, factor):
+    """K1 multiplying by a scale_grads factor (MS_SCALE_MULTIPLY): a tile's
+    flag is set exactly when one of its raw gradients is inf/nan — also
+    where the factor turns finite gradients into inf (|factor| > 1, where
+    the kernel tests every word) or an inf into nan (0); with the factor in
+    [-1, 1] the flags of the counted elements come from their sums."""
+    lib = _native.load()
+    tile = _native.SCAN_TILE
+    n = 7 * tile + 100
+    g = torch.full((n,), 1e3 if dtype == F16 else 1e10, dtype=torch.float32)
+    g[::7] *= -1.0
+    g[2 * tile + 5] = float("inf")
+    g[4 * tile + tile - 1] = float("nan")
+    g[6 * tile + 3] = -float("inf")
+    dg = g.to(dtype).to(DEV)
+    lay = layout_for([n])
+    tab = Table(lay, 0, n, [store(dg, 0)], [None])
+    nb, nt = _native.stats_blocks(), _native.scan_tiles(n)
+    psum = torch.empty(nb, dtype=torch.float64, device=DEV)
+    pflag = torch.empty(nb, dtype=torch.int32, device=DEV)
+    tsum = torch.empty(nt, dtype=torch.float64, device=DEV)
+    tflag = torch.full((nt,), -1, dtype=torch.int32, device=DEV)
+    for lo, hi in ((0, n), (tile + 7, 5 * tile)):      # counted everywhere / partly
+        _native.check(lib.ms_grad_stats(tab.ptr, tab.nseg, _native.ms_dtype(dtype), 0, n, lo, hi,
+                                        _native.SCALE_MULTIPLY, float(np.float32(factor)), None,
+                                        tsum.data_ptr(), tflag.data_ptr(), nt, psum.data_ptr(),
+                                        pflag.data_ptr(), nb, stream()), "ms_grad_stats")
+        torch.cuda.synchronize()
+        raw_bad = ~torch.isfinite(dg.float().cpu())
+        want = [int(raw_bad[t * tile:(t + 1) * tile].any()) for t in range(nt)]
+        assert [int(f != 0) for f in tflag.cpu().tolist()] == want, (lo, hi)
+
+
 def test_k2_host_copy_equals_device_result_after_an_event():
     """K2's optional host-side output (pinned memory written by the kernel)
     holds the device result, with ``ready`` set, once an event recorded
