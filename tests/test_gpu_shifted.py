@@ -10,6 +10,8 @@ rounds predicated; when writing the flat gradient, the tile split over
 the block's four waves with its head and tail staged in LDS; K3 /
 K4 / K5: quads of any alignment).  Checked here:
 
+* K1's pure flatten (the initial master copy) of shifted tensors of whole
+  tiles, bit for bit;
 * K1 for every head length and dtype: the flat gradient bit for bit against
   the widened, scaled gradients, every tile flag exactly, tile sums within
   1e-12 of the exact sum of squares, and the statistics bit for bit the same
@@ -117,6 +119,39 @@ def test_k1_every_head_length(dtype, head):
             if not bad[a:b].any():
                 exact = recipe.sumsq_f64(owned[a:b].astype(np.float32))
                 assert abs(ts[t] - exact) <= 1e-12 * exact, t
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+@pytest.mark.parametrize("head", [1, 3, 5, 6])
+def test_k1_flatten_only_of_shifted_tensors(dtype, head):
+    """The pure ragged flatten (no statistics, as copy_model_to_flat) over
+    tensors of whole tiles behind a `head`-element one, over the whole flat
+    space and over a sub-range that starts off the tile grid: every output
+    element is the widened source, bit for bit, and nothing past the range
+    is written."""
+    sizes = [head, 5 * TILE + 3, 3 * TILE, 77, 4 * TILE + 1, 2 * TILE]
+    gen = torch.Generator().manual_seed(31 + head)
+    host = [torch.randn(k, generator=gen).to(dtype) for k in sizes]
+    _, views = _views(sizes, dtype, [0] * len(sizes))
+    for v, h in zip(views, host):
+        v.copy_(h.to(DEV))
+    lay = layout_for(sizes)
+    n = lay.numel_padded
+    full = torch.zeros(n)
+    for h, off in zip(host, lay.offsets):
+        full[off:off + h.numel()] = h.float()
+    gst = [store(v, off) for v, off in zip(views, lay.offsets)]
+    lib = _native.load()
+    for lo, hi in ((0, n), (TILE + 5, n - TILE - 3)):
+        tab = Table(lay, lo, hi, gst, [None] * len(sizes))
+        flat = torch.full((hi - lo + 64,), float("nan"), device=DEV)
+        _native.check(lib.ms_grad_stats(tab.ptr, tab.nseg, _native.ms_dtype(dtype), lo, hi, lo, hi,
+                                        0, 1.0, flat.data_ptr(), None, None, 0, None, None, 0,
+                                        _native.stream_handle(torch.device(DEV))), "flatten")
+        torch.cuda.synchronize()
+        got = flat.cpu()
+        np.testing.assert_array_equal(bits(got[:hi - lo]), bits(full[lo:hi]))
+        assert torch.isnan(got[hi - lo:]).all(), "wrote past the range"
 
 
 COMBOS = [(F16, F16), (BF16, BF16), (F32, F32), (F16, F32), (F32, BF16), (BF16, F16)]
